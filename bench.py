@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|mixed|flash]
+                    [--no-cpu-baseline]
+
+Headline (``value``): paged decode attention, bf16, Qwen3-0.6B attention
+shape (16 query heads, 8 KV heads, head_dim 128, 16-token pages), 64
+sequences with contexts U[256, 4096] scattered over a pool 1.2x the used
+blocks.  One step = one ``femtovllm.ops.paged_attention_gemv`` call over the
+batch.  ``value`` = algorithmic HBM bytes (K and V once per KV head, Q, O,
+block-table entries, kv_lens) / mean kernel time, in GB/s.
+
+Timing: every step is [L2/MALL flush by a 1 GiB write][spin][start event]
+[op][end event] on torch's current stream, the stream the op launches its
+kernel on; ``ms_per_step`` is the mean start->end time over K steps after W
+warm-up steps, bracketed by torch.cuda.synchronize().  Inputs are resident
+in HBM before timing starts.
+
+Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
+long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
+sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
+dense flash-attention latencies at the reference benchmark shapes.
+``cpu_baseline``: the reference's CPU attention path (per-sequence block
+gather + torch SDPA, restated in oracle/sdpa_path.py) timed on the host in
+the workload dtype.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "nano-vllm-practice_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="all", choices=["all", "decode", "prefill", "long", "mixed", "flash"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+class Timer:
+    """Per-step kernel timing with HIP events on torch's current stream."""
+
+    def __init__(self, torch, device):
+        self.torch = torch
+        self.flush = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        evs = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self.flush.zero_()
+            torch.cuda._sleep(200_000)
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            evs.append((s, e))
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = [s.elapsed_time(e) for s, e in evs]
+        return statistics.fmean(ms), statistics.median(ms), wall
+
+
+def pmc_traffic(kernel_key):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if present."""
+    path = os.path.join(PROFILES, f"{kernel_key}_pmc.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def cpu_baseline_decode(w, sample_s=12.0):
+    """The reference CPU path on the decode batch, bf16, all host threads."""
+    import torch
+
+    from oracle import sdpa_path
+    from femtovllm import workloads
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    q, meta = w.gemv_call(device="cpu")
+    args = (q, w.k_pool, w.v_pool, meta.raw_block_tables, meta.raw_kv_lens)
+    sdpa_path.paged_decode(*args)  # warm
+    times = []
+    t_end = time.perf_counter() + sample_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        sdpa_path.paged_decode(*args)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    nbytes = workloads.decode_bytes(w)
+    return {
+        "value": round(nbytes / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"whole decode batch (64 seqs), {len(times)} reps, median {t * 1e3:.1f} ms; "
+                  "per-sequence block gather + torch SDPA, bf16",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py: --gpus {args.gpus} is not supported: the attention path is measured on one GPU "
+            "(the reference engine is single-GPU; across GPUs the path shards by KV head or by sequence "
+            "with no exchange inside attention).",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from femtovllm import ops, workloads
+    from femtovllm import _C
+
+    dev = torch.device("cuda:0")
+    timer = Timer(torch, dev)
+    K, W = args.steps, args.warmup
+    extra = []
+    result = None
+
+    def want(name):
+        return args.only in ("all", name)
+
+    # ---------------- headline: decode ------------------------------------
+    if want("decode"):
+        w = workloads.decode_bf16_qwen3_0p6b(poison=False)
+        wd = w.to(dev)
+        q, meta = wd.gemv_call(device=dev)
+        fn = lambda: ops.paged_attention_gemv(q, wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
+                                              meta.max_kv_len)
+        out = fn()
+        torch.cuda.synchronize()
+        assert not torch.isnan(out.float()).any(), "decode produced NaN"
+        mean_ms, med_ms, wall = timer.run(fn, K, W)
+        nbytes = workloads.decode_bytes(w)
+        gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        result = {
+            "metric": "paged decode attention HBM bandwidth (bf16, Qwen3-0.6B shape, B=64, ctx U[256,4096])",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "steps": K,
+            "warmup": W,
+            "ms_per_step": round(mean_ms, 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic (seeded N(0,1) q/k/v, random block placement)",
+            "config": {
+                "workload": "paged_decode_bf16_qwen3_0.6b_b64_ctx256-4096",
+                "num_seqs": 64,
+                "n_heads": 16,
+                "n_kv_heads": 8,
+                "head_dim": 128,
+                "block_size": 16,
+                "total_kv_tokens": int(meta.kv_lens.sum().item()),
+                "pool_blocks": int(w.k_pool.shape[0]),
+                "parallelism": "single GPU",
+            },
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(gbs, 2),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": pmc_traffic("paged_decode_bf16_qwen3_0.6b_b64"),
+                "algorithmic_bytes_per_launch": nbytes,
+                "kernel": "paged_decode_kernel<BF16,2>",
+            },
+            "median_ms_per_step": round(med_ms, 5),
+            "wall_s_timed_region": round(wall, 3),
+        }
+        del wd
+        if not args.no_cpu_baseline:
+            result["cpu_baseline"] = cpu_baseline_decode(w)
+        del w
+
+    # ---------------- prefill: 8 x 512 chunks -----------------------------
+    if want("prefill"):
+        w = workloads.prefill_bf16_chunked(poison=False)
+        wd = w.to(dev)
+        q, meta = wd.gemm_call(device=dev)
+        fn = lambda: ops.paged_attention_gemm(q, wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len,
+                                              meta.Q_TILE_SIZE, meta.cu_q_tiles, meta.q_tile_to_seq_idx,
+                                              meta.block_tables, meta.kv_lens, meta.positions)
+        mean_ms, med_ms, _ = timer.run(fn, K, W)
+        flops = workloads.prefill_flops(w.chunks, w.n_heads, w.head_dim)
+        tf = flops / (mean_ms * 1e-3) / 1e12
+        extra.append({
+            "workload": "chunked_prefill_bf16_8x512_prefix0-2048_h16_kv8",
+            "metric": "TFLOP/s (causal-exact)", "value": round(tf, 2), "ms": round(mean_ms, 5),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops},
+        })
+        del wd, w
+
+    # ---------------- long context: 16 x 2048 chunks ----------------------
+    if want("long"):
+        w = workloads.prefill_bf16_long_llama3_8b(poison=False)
+        wd = w.to(dev)
+        calls = []
+        for c in range(16):
+            q, meta = workloads.long_context_chunk(wd, c, device=dev)
+            calls.append((q, meta))
+
+        def fn():
+            for q, meta in calls:
+                ops.paged_attention_gemm(q, wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len, meta.Q_TILE_SIZE,
+                                         meta.cu_q_tiles, meta.q_tile_to_seq_idx, meta.block_tables, meta.kv_lens,
+                                         meta.positions)
+
+        steps = max(1, K // 4)
+        mean_ms, med_ms, _ = timer.run(fn, steps, max(1, W // 2))
+        flops = workloads.prefill_flops([(2048 * c, 2048) for c in range(16)], 32, 128)
+        tf = flops / (mean_ms * 1e-3) / 1e12
+        extra.append({
+            "workload": "long_context_prefill_bf16_llama3_8b_32k_as_16x2048",
+            "metric": "TFLOP/s (causal-exact, 16 calls)", "value": round(tf, 2), "ms": round(mean_ms, 4),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": flops},
+        })
+        del wd, w, calls
+
+    # ---------------- unified mixed batch ---------------------------------
+    if want("mixed"):
+        w = workloads.mixed_bf16_qwen3_8b(poison=False)
+        wd = w.to(dev)
+        qp, mp = wd.gemm_call(seqs=[0], device=dev)
+        qd, md = wd.gemv_call(seqs=range(1, 128), device=dev)
+        qa, ma = wd.gemm_call(device=dev)
+
+        def route_split():
+            ops.paged_attention_gemm(qp, wd.k_pool, wd.v_pool, mp.cu_seqlens, mp.max_q_len, mp.Q_TILE_SIZE,
+                                     mp.cu_q_tiles, mp.q_tile_to_seq_idx, mp.block_tables, mp.kv_lens, mp.positions)
+            ops.paged_attention_gemv(qd, wd.k_pool, wd.v_pool, md.block_tables, md.kv_lens, md.max_kv_len)
+
+        def route_unified():
+            ops.paged_attention_gemm(qa, wd.k_pool, wd.v_pool, ma.cu_seqlens, ma.max_q_len, ma.Q_TILE_SIZE,
+                                     ma.cu_q_tiles, ma.q_tile_to_seq_idx, ma.block_tables, ma.kv_lens, ma.positions)
+
+        ms_split, _, _ = timer.run(route_split, K, W)
+        ms_uni, _, _ = timer.run(route_unified, K, W)
+        dec_bytes = workloads.decode_bytes(w, seqs=range(1, 128))
+        dec_bytes_logical = workloads.decode_bytes(w, seqs=range(1, 128), unique_blocks=False)
+        flops = workloads.prefill_flops([w.chunks[0]], 32, 128)
+        extra.append({
+            "workload": "mixed_bf16_qwen3_8b_1x1024on4096_plus_127_decode",
+            "ms_prefill_plus_decode": round(ms_split, 4),
+            "ms_single_gemm_call": round(ms_uni, 4),
+            "prefill_flops": flops, "decode_unique_bytes": dec_bytes, "decode_logical_bytes": dec_bytes_logical,
+        })
+        del wd, w
+
+    # ---------------- dense flash attention (reference benchmark shapes) --
+    if want("flash"):
+        lat = {}
+        for T in (16, 32, 64, 128, 256):
+            g = torch.Generator().manual_seed(T)
+            qkv = [torch.randn((2, 4, T, 128), generator=g).half().to(dev) for _ in range(3)]
+            fn = lambda: _C.FlashAttentionWarpCuda(*qkv)
+            mean_ms, _, _ = timer.run(fn, K, W)
+            lat[str(T)] = round(mean_ms, 5)
+        extra.append({"workload": "dense_flash_attention_fp16_B2_H4_D128_noncausal", "ms_by_seq_len": lat})
+
+    if result is None:
+        result = {"metric": f"bench subset '{args.only}'", "value": None, "unit": None, "n_gpus": 1, "steps": K,
+                  "warmup": W}
+    result["extra"] = extra
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,116 @@
+/*
+ * femto_attn.h -- C ABI of libfemto_attn.so, the MI355X (gfx950) attention
+ * hot path of FemtoVLLM (fishAndShrimp/nano-vllm-practice).
+ *
+ * Every entry point takes raw device pointers, element strides and sizes,
+ * launches hand-written HIP kernels on the given stream (a hipStream_t
+ * passed as void*, NULL = the null stream) and returns without
+ * synchronising.  No entry point allocates device memory: outputs and the
+ * decode workspace belong to the caller.  Inputs are read-only; the KV pools
+ * are never written except by femto_paged_kv_cache_write.
+ *
+ * Return value: FEMTO_OK, or an error code with a message available from
+ * femto_attn_last_error() (thread-local, valid until the next call on the
+ * same thread).
+ *
+ * Layouts (all strides in elements, innermost dimension contiguous):
+ *   paged pool  (num_blocks, n_kv_heads, block_size = 16, head_dim = 128)
+ *   block table (num_seqs, num_pages_per_seq) int32, -1 padded
+ *   decode q/out  (n_heads, num_seqs, head_dim)
+ *   prefill q/out (n_heads, num_tokens, head_dim), sequences by cu_seqlens
+ *   dense q/out (batch, n_heads, q_len, head_dim), k/v (batch, n_kv_heads, kv_len, head_dim)
+ */
+#ifndef FEMTO_ATTN_H_
+#define FEMTO_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum femto_status {
+    FEMTO_OK = 0,
+    FEMTO_ERR_INVALID = 1,     /* shape / stride / value check failed     */
+    FEMTO_ERR_UNSUPPORTED = 2, /* dtype or size this library does not run */
+    FEMTO_ERR_HIP = 3          /* HIP runtime error from a launch         */
+};
+
+enum femto_dtype { FEMTO_F32 = 0, FEMTO_F16 = 1, FEMTO_BF16 = 2 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* femto_attn_last_error(void);
+
+/* Compile-time constants the reference exports as _C attributes
+ * (csrc/bindings.cpp:62-66 <- csrc/utils/constants.cuh:8, 39, 75):
+ * kMaxKVLenNonSplit = 8192, kKVLenPerPage = 16, kDimHead = 128. */
+int femto_attn_max_kv_len_non_split(void);
+int femto_attn_kv_len_per_page(void);
+int femto_attn_dim_head(void);
+
+/* Bytes of workspace femto_paged_attention_gemv needs for these sizes.
+ * The workspace must be zero-filled before its first use; every call
+ * leaves its counter section zeroed again, so one buffer can be reused by
+ * calls that are ordered on one stream (calls that overlap must not share
+ * a workspace). */
+size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len);
+
+/* Paged decode attention: one query token per sequence attends to all
+ * kv_lens[b] keys of its block table; GQA kv head = h / (n_heads / n_kv_heads).
+ * Replaces PagedAttentionGemvCuda (csrc/paged_attention/paged_attention_gemv.cu:223-308),
+ * bound as _C.PagedAttentionGemvCuda (csrc/bindings.cpp:52-59, 94-97) and
+ * called by femtovllm.ops.paged_attention_gemv (femtovllm/ops/__init__.py:82-107).
+ * dtype: F32, F16 or BF16.  kv_len == 0 yields a zero row, as in the reference. */
+int femto_paged_attention_gemv(
+    int dtype,
+    const void* q, int64_t q_stride_head, int64_t q_stride_seq,
+    void* out, int64_t out_stride_head, int64_t out_stride_seq,
+    const void* k_pool, const void* v_pool,
+    int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
+    int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+    const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+    const int32_t* kv_lens, int num_seqs, int n_heads, int max_kv_len,
+    void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* Paged chunked / varlen / causal prefill attention on bf16 or f16 MFMA:
+ * token t of sequence b (cu_seqlens[b] <= t < cu_seqlens[b+1]) sees key j
+ * iff j < kv_lens[b] and j <= positions[t].
+ * Replaces PagedAttentionGemmCuda (csrc/paged_attention/paged_attention_gemm.cu:304-395)
+ * and paged_attention_gemm_triton
+ * (femtovllm/ops/triton/paged_attention/paged_attention_gemm.py:165-235),
+ * bound as _C.PagedAttentionGemmCuda (csrc/bindings.cpp:41-50, 90-93) and
+ * called by femtovllm.ops.paged_attention_gemm (femtovllm/ops/__init__.py:110-156).
+ * dtype: F16 or BF16 (the reference kernels reject F32 too).  A row with
+ * no visible key (kv_len == 0) is NaN, as in the reference. */
+int femto_paged_attention_gemm(
+    int dtype,
+    const void* q, int64_t q_stride_head, int64_t q_stride_token,
+    void* out, int64_t out_stride_head, int64_t out_stride_token,
+    const void* k_pool, const void* v_pool,
+    int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
+    int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+    const int32_t* cu_seqlens, int num_seqs, int num_tokens, int n_heads,
+    const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+    const int32_t* kv_lens, const int32_t* positions,
+    void* stream);
+
+/* Dense non-causal GQA flash attention, q (B, H, Tq, D), k/v (B, KVH, Tkv, D).
+ * Replaces FlashAttentionWarpCuda (csrc/flash_attention/flash_attention_warp.cu:301-376),
+ * bound as _C.FlashAttentionWarpCuda (csrc/bindings.cpp:35-39, 86-89).
+ * dtype: F16 or BF16. */
+int femto_flash_attention(
+    int dtype,
+    const void* q, int64_t q_stride_batch, int64_t q_stride_head, int64_t q_stride_token,
+    const void* k, int64_t k_stride_batch, int64_t k_stride_head, int64_t k_stride_token,
+    const void* v, int64_t v_stride_batch, int64_t v_stride_head, int64_t v_stride_token,
+    void* out, int64_t out_stride_batch, int64_t out_stride_head, int64_t out_stride_token,
+    int batch, int n_heads, int n_kv_heads, int q_len, int kv_len, int head_dim,
+    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FEMTO_ATTN_H_ */

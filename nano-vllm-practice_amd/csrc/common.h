@@ -1,0 +1,119 @@
+// Device helpers shared by the gfx950 attention kernels.
+//
+// Wavefronts are 64 lanes.  A "row" below is a DPP row of 16 lanes; the
+// decode kernel assigns one key (16 lanes x 8 head dims) per row, so its
+// dot-product reduction never leaves a DPP row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace femto {
+
+constexpr int kPage = 16;               // tokens per KV page (kKVLenPerPage)
+constexpr int kDimHead = 128;           // head dim the kernels are built for
+constexpr int kMaxKVLenNonSplit = 8192; // exported for API parity
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// log2(e): softmax runs in base 2, exp(x) = exp2(x * log2(e)).
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- DPP all-reduce inside a 16-lane row -------------------------------
+// row_ror:8, row_ror:4, quad_perm [2,3,0,1], quad_perm [1,0,3,2]: after the
+// four steps every lane of the row holds the row total.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f32<0x128>(x);  // row_ror:8
+    x += dpp_f32<0x124>(x);  // row_ror:4
+    x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+    return x;
+}
+
+__device__ __forceinline__ float shfl_xor_f32(float x, int mask) { return __shfl_xor(x, mask, kWave); }
+
+// ---- element types -----------------------------------------------------
+struct BF16 {
+    using mfma_vec = bf16x8;
+    using quad = bf16x4;
+    static constexpr int kBytes = 2;
+};
+struct F16 {
+    using mfma_vec = f16x8;
+    using quad = f16x4;
+    static constexpr int kBytes = 2;
+};
+struct F32 {
+    static constexpr int kBytes = 4;
+};
+
+// 8 x 16-bit values held in a 16-byte register quad.
+__device__ __forceinline__ void unpack8(BF16, u32x4 w, float f[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = __uint_as_float(w[i] << 16);
+        f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ void unpack8(F16, u32x4 w, float f[8]) {
+    f16x8 h = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = (float)h[i];
+}
+
+// Round-to-nearest-even conversion of 8 floats to 16-bit storage.
+__device__ __forceinline__ u32x4 pack8(BF16, const float f[8]) {
+    bf16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (__bf16)f[i];
+    return __builtin_bit_cast(u32x4, h);
+}
+
+__device__ __forceinline__ u32x4 pack8(F16, const float f[8]) {
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (_Float16)f[i];
+    return __builtin_bit_cast(u32x4, h);
+}
+
+__device__ __forceinline__ u32x2 pack4(BF16, float a, float b, float c, float d) {
+    bf16x4 h = {(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+    return __builtin_bit_cast(u32x2, h);
+}
+
+__device__ __forceinline__ u32x2 pack4(F16, float a, float b, float c, float d) {
+    f16x4 h = {(_Float16)a, (_Float16)b, (_Float16)c, (_Float16)d};
+    return __builtin_bit_cast(u32x2, h);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(BF16, u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(F16, u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+}  // namespace femto

@@ -1,0 +1,302 @@
+// C ABI of libfemto_attn.so: argument checks, launch planning, dispatch.
+//
+// The checks mirror the reference host wrappers
+// (csrc/paged_attention/paged_attention_gemv.cu:231-274,
+// csrc/paged_attention/paged_attention_gemm.cu:314-353,
+// csrc/flash_attention/flash_attention_warp.cu:306-349) for what can be seen
+// from raw pointers and sizes; tensor-level checks (device, rank, int32
+// index dtype) live in the Python layer that owns the tensors.
+#include <cmath>
+#include <cstdlib>
+#include <string>
+
+#include "common.h"
+#include "femto_attn.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return FEMTO_OK;
+    return fail(FEMTO_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; }
+
+const char* dtype_name(int dtype) {
+    switch (dtype) {
+        case FEMTO_F32: return "Float";
+        case FEMTO_F16: return "Half";
+        case FEMTO_BF16: return "BFloat16";
+        default: return "unknown";
+    }
+}
+
+int elem_bytes(int dtype) { return dtype == FEMTO_F32 ? 4 : 2; }
+
+float scale_log2(int head_dim) { return femto::kLog2e / std::sqrt((float)head_dim); }
+
+int env_int(const char* name, int fallback) {
+    const char* s = std::getenv(name);
+    if (!s || !*s) return fallback;
+    const int v = std::atoi(s);
+    return v > 0 ? v : fallback;
+}
+
+}  // namespace
+
+namespace femto {
+
+DecodePlan plan_paged_decode(int num_seqs, int n_heads, int n_kv_heads, int max_kv_len) {
+    DecodePlan p;
+    const int n_rep = (n_kv_heads > 0) ? n_heads / n_kv_heads : 1;
+    p.nrep_tile = (n_rep % 8 == 0) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
+    const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
+    // Pages per workgroup: the smallest power of two (8..256) that keeps
+    // the estimated number of workgroups (average context = max / 2, two
+    // query heads per KV head) at or below 4096, i.e. a few per CU in
+    // flight with a small split-merge overhead.
+    int sp = env_int("FEMTO_DECODE_SPLIT_PAGES", 0);
+    if (sp == 0) {
+        const double est = (double)num_seqs * (max_pages / 2.0) * (n_heads / 2.0 > 1.0 ? n_heads / 2.0 : 1.0);
+        sp = 8;
+        while (sp < 256 && est / sp > 4096.0) sp *= 2;
+    }
+    p.split_pages = sp;
+    p.max_splits = (max_pages + sp - 1) / sp;
+    if (p.max_splits < 1) p.max_splits = 1;
+    return p;
+}
+
+size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_splits) {
+    if (max_splits <= 1) return 0;
+    const size_t slots = (size_t)num_seqs * n_heads * max_splits;
+    size_t bytes = slots * kDimHead * sizeof(float);
+    bytes += slots * 2 * sizeof(float);
+    bytes = (bytes + 255) & ~size_t(255);
+    bytes += (size_t)num_seqs * n_heads * sizeof(int);
+    return bytes;
+}
+
+}  // namespace femto
+
+extern "C" {
+
+const char* femto_attn_last_error(void) { return g_err.c_str(); }
+
+int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
+int femto_attn_kv_len_per_page(void) { return femto::kPage; }
+int femto_attn_dim_head(void) { return femto::kDimHead; }
+
+size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
+    if (num_seqs <= 0 || n_heads <= 0) return 0;
+    const femto::DecodePlan p = femto::plan_paged_decode(num_seqs, n_heads, 1, max_kv_len);
+    return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_splits);
+}
+
+static int check_paged_common(const char* fn, int dtype, const void* q, const void* out, const void* k_pool,
+                              const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
+                              int head_dim, int64_t ps0, int64_t ps1, int64_t ps2, int n_heads,
+                              int64_t q_s0, int64_t q_s1, const int32_t* tables, int num_pages_per_seq,
+                              int64_t table_stride) {
+    std::string f(fn);
+    if (head_dim != femto::kDimHead)
+        return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be " + std::to_string(femto::kDimHead) + ", got " +
+                                               std::to_string(head_dim));
+    if (block_size != femto::kPage)
+        return fail(FEMTO_ERR_INVALID, f + ": block_size must be " + std::to_string(femto::kPage) + ", got " +
+                                           std::to_string(block_size));
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0)
+        return fail(FEMTO_ERR_INVALID, f + ": n_heads (" + std::to_string(n_heads) +
+                                           ") must be a positive multiple of n_kv_heads (" +
+                                           std::to_string(n_kv_heads) + ")");
+    if (num_blocks < 0 || num_pages_per_seq < 0 || table_stride < 0)
+        return fail(FEMTO_ERR_INVALID, f + ": negative pool or table size");
+    if (!q || !out || !k_pool || !v_pool || (num_pages_per_seq > 0 && !tables))
+        return fail(FEMTO_ERR_INVALID, f + ": null pointer argument");
+    const int vec = 16 / elem_bytes(dtype);
+    if (!aligned(q, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16) || !aligned(out, 8))
+        return fail(FEMTO_ERR_INVALID, f + ": q, k_pool and v_pool must be 16-byte aligned, out 8-byte aligned");
+    if (ps0 % vec || ps1 % vec || ps2 % vec || q_s0 % vec || q_s1 % vec)
+        return fail(FEMTO_ERR_INVALID, f + ": pool and q strides must be multiples of 16 bytes");
+    return FEMTO_OK;
+}
+
+int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_seq, void* out,
+                               int64_t out_stride_head, int64_t out_stride_seq, const void* k_pool,
+                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
+                               int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
+                               int64_t pool_stride_row, const int32_t* kv_page_tables, int num_pages_per_seq,
+                               int64_t table_stride, const int32_t* kv_lens, int num_seqs, int n_heads,
+                               int max_kv_len, void* workspace, size_t workspace_bytes, void* stream) {
+    g_err.clear();
+    if (dtype != FEMTO_F32 && dtype != FEMTO_F16 && dtype != FEMTO_BF16)
+        return fail(FEMTO_ERR_UNSUPPORTED, std::string("paged_attention_gemv: dtype ") + dtype_name(dtype) +
+                                               " is not supported");
+    if (num_seqs < 0 || max_kv_len < 0) return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: negative size");
+    if (num_seqs == 0) return FEMTO_OK;
+    if (!kv_lens) return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: null kv_lens");
+    int rc = check_paged_common("paged_attention_gemv", dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
+                                block_size, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, n_heads,
+                                q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride);
+    if (rc != FEMTO_OK) return rc;
+
+    const femto::DecodePlan plan = femto::plan_paged_decode(num_seqs, n_heads, n_kv_heads, max_kv_len);
+    const size_t need = femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_splits);
+    if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
+        return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: workspace of " + std::to_string(need) +
+                                           " bytes (256-byte aligned, zero-filled before first use) required, got " +
+                                           std::to_string(workspace_bytes));
+
+    femto::DecodeArgs a{};
+    a.q = q;
+    a.q_stride_head = q_stride_head;
+    a.q_stride_seq = q_stride_seq;
+    a.out = out;
+    a.out_stride_head = out_stride_head;
+    a.out_stride_seq = out_stride_seq;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.num_blocks = num_blocks;
+    a.pool_stride_block = pool_stride_block;
+    a.pool_stride_head = pool_stride_head;
+    a.pool_stride_row = pool_stride_row;
+    a.tables = kv_page_tables;
+    a.table_stride = table_stride;
+    a.num_pages_per_seq = num_pages_per_seq;
+    a.kv_lens = kv_lens;
+    a.n_heads = n_heads;
+    a.n_rep = n_heads / n_kv_heads;
+    a.head_groups = a.n_rep / plan.nrep_tile;
+    a.split_pages = plan.split_pages;
+    a.max_splits = plan.max_splits;
+    a.scale_log2 = scale_log2(head_dim);
+    if (need > 0) {
+        char* ws = static_cast<char*>(workspace);
+        const size_t slots = (size_t)num_seqs * n_heads * plan.max_splits;
+        a.part_acc = reinterpret_cast<float*>(ws);
+        a.part_ml = reinterpret_cast<float*>(ws + slots * femto::kDimHead * sizeof(float));
+        size_t coff = slots * (femto::kDimHead + 2) * sizeof(float);
+        coff = (coff + 255) & ~size_t(255);
+        a.counters = reinterpret_cast<int*>(ws + coff);
+    }
+    return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, plan.max_splits, num_seqs,
+                                                 static_cast<hipStream_t>(stream)),
+                      "paged_attention_gemv launch");
+}
+
+int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_token, void* out,
+                               int64_t out_stride_head, int64_t out_stride_token, const void* k_pool,
+                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
+                               int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
+                               int64_t pool_stride_row, const int32_t* cu_seqlens, int num_seqs, int num_tokens,
+                               int n_heads, const int32_t* kv_page_tables, int num_pages_per_seq,
+                               int64_t table_stride, const int32_t* kv_lens, const int32_t* positions,
+                               void* stream) {
+    g_err.clear();
+    if (dtype != FEMTO_F16 && dtype != FEMTO_BF16)
+        return fail(FEMTO_ERR_UNSUPPORTED, std::string("paged_attention_gemm: not implemented for '") +
+                                               dtype_name(dtype) + "' (bf16 / f16 MFMA only)");
+    if (num_seqs < 0 || num_tokens < 0) return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: negative size");
+    if (num_seqs == 0 || num_tokens == 0) return FEMTO_OK;
+    if (!cu_seqlens || !kv_lens || !positions)
+        return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: null cu_seqlens / kv_lens / positions");
+    int rc = check_paged_common("paged_attention_gemm", dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
+                                block_size, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, n_heads,
+                                q_stride_head, q_stride_token, kv_page_tables, num_pages_per_seq, table_stride);
+    if (rc != FEMTO_OK) return rc;
+    if (out_stride_head % 4 || out_stride_token % 4)
+        return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: out strides must be multiples of 8 bytes");
+
+    femto::PrefillArgs a{};
+    a.q = q;
+    a.q_stride_batch = 0;
+    a.q_stride_head = q_stride_head;
+    a.q_stride_token = q_stride_token;
+    a.out = out;
+    a.out_stride_batch = 0;
+    a.out_stride_head = out_stride_head;
+    a.out_stride_token = out_stride_token;
+    a.k = k_pool;
+    a.v = v_pool;
+    a.k_stride0 = a.v_stride0 = pool_stride_block;
+    a.k_stride1 = a.v_stride1 = pool_stride_head;
+    a.k_stride2 = a.v_stride2 = pool_stride_row;
+    a.num_blocks = num_blocks;
+    a.cu_seqlens = cu_seqlens;
+    a.tables = kv_page_tables;
+    a.table_stride = table_stride;
+    a.num_pages_per_seq = num_pages_per_seq;
+    a.kv_lens = kv_lens;
+    a.positions = positions;
+    a.num_seqs = num_seqs;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.n_rep = n_heads / n_kv_heads;
+    a.scale_log2 = scale_log2(head_dim);
+    return hip_status(femto::launch_paged_prefill(dtype, a, num_tokens, static_cast<hipStream_t>(stream)),
+                      "paged_attention_gemm launch");
+}
+
+int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int64_t q_stride_head,
+                          int64_t q_stride_token, const void* k, int64_t k_stride_batch, int64_t k_stride_head,
+                          int64_t k_stride_token, const void* v, int64_t v_stride_batch, int64_t v_stride_head,
+                          int64_t v_stride_token, void* out, int64_t out_stride_batch, int64_t out_stride_head,
+                          int64_t out_stride_token, int batch, int n_heads, int n_kv_heads, int q_len, int kv_len,
+                          int head_dim, void* stream) {
+    g_err.clear();
+    if (dtype != FEMTO_F16 && dtype != FEMTO_BF16)
+        return fail(FEMTO_ERR_UNSUPPORTED, std::string("flash_attention: not implemented for '") + dtype_name(dtype) +
+                                               "' (bf16 / f16 MFMA only)");
+    if (head_dim != femto::kDimHead)
+        return fail(FEMTO_ERR_UNSUPPORTED, "flash_attention: head_dim must be " + std::to_string(femto::kDimHead));
+    if (batch < 0 || q_len < 0 || kv_len < 0) return fail(FEMTO_ERR_INVALID, "flash_attention: negative size");
+    if (n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0)
+        return fail(FEMTO_ERR_INVALID, "flash_attention: n_heads must be a positive multiple of n_kv_heads");
+    if (batch == 0 || q_len == 0) return FEMTO_OK;
+    if (!q || !k || !v || !out) return fail(FEMTO_ERR_INVALID, "flash_attention: null pointer argument");
+    if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(out, 8))
+        return fail(FEMTO_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned, out 8-byte aligned");
+    const int64_t st[] = {q_stride_batch, q_stride_head, q_stride_token, k_stride_batch, k_stride_head,
+                          k_stride_token, v_stride_batch, v_stride_head, v_stride_token};
+    for (int64_t s : st)
+        if (s % 8) return fail(FEMTO_ERR_INVALID, "flash_attention: q/k/v strides must be multiples of 16 bytes");
+    if (out_stride_batch % 4 || out_stride_head % 4 || out_stride_token % 4)
+        return fail(FEMTO_ERR_INVALID, "flash_attention: out strides must be multiples of 8 bytes");
+
+    femto::PrefillArgs a{};
+    a.q = q;
+    a.q_stride_batch = q_stride_batch;
+    a.q_stride_head = q_stride_head;
+    a.q_stride_token = q_stride_token;
+    a.out = out;
+    a.out_stride_batch = out_stride_batch;
+    a.out_stride_head = out_stride_head;
+    a.out_stride_token = out_stride_token;
+    a.k = k;
+    a.v = v;
+    a.k_stride0 = k_stride_batch;
+    a.k_stride1 = k_stride_head;
+    a.k_stride2 = k_stride_token;
+    a.v_stride0 = v_stride_batch;
+    a.v_stride1 = v_stride_head;
+    a.v_stride2 = v_stride_token;
+    a.num_seqs = batch;
+    a.q_len = q_len;
+    a.kv_len = kv_len;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.n_rep = n_heads / n_kv_heads;
+    a.scale_log2 = scale_log2(head_dim);
+    return hip_status(femto::launch_dense_attention(dtype, a, static_cast<hipStream_t>(stream)),
+                      "flash_attention launch");
+}
+
+}  // extern "C"

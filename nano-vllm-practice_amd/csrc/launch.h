@@ -1,0 +1,73 @@
+// Kernel argument blocks and launchers (host side of the HIP kernels).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace femto {
+
+enum { kDtypeF32 = 0, kDtypeF16 = 1, kDtypeBF16 = 2 };
+
+struct DecodeArgs {
+    const void* q;
+    int64_t q_stride_head, q_stride_seq;
+    void* out;
+    int64_t out_stride_head, out_stride_seq;
+    const void* k_pool;
+    const void* v_pool;
+    int64_t num_blocks;
+    int64_t pool_stride_block, pool_stride_head, pool_stride_row;
+    const int32_t* tables;
+    int64_t table_stride;
+    int num_pages_per_seq;
+    const int32_t* kv_lens;
+    int n_heads, n_rep, head_groups;
+    int split_pages, max_splits;
+    float scale_log2;
+    float* part_acc;  // [num_seqs][n_heads][max_splits][128]
+    float* part_ml;   // [num_seqs][n_heads][max_splits][2]
+    int* counters;    // [num_seqs][n_heads / nrep_tile]
+};
+
+// Split size (pages per workgroup) and split count used for a decode call.
+struct DecodePlan {
+    int nrep_tile;   // query heads per workgroup
+    int split_pages;
+    int max_splits;  // grid.x
+};
+DecodePlan plan_paged_decode(int num_seqs, int n_heads, int n_kv_heads, int max_kv_len);
+size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_splits);
+
+hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int grid_splits, int num_seqs,
+                               hipStream_t st);
+
+struct PrefillArgs {
+    const void* q;
+    int64_t q_stride_batch, q_stride_head, q_stride_token;
+    void* out;
+    int64_t out_stride_batch, out_stride_head, out_stride_token;
+    const void* k;
+    const void* v;
+    // paged: block / kv head / row strides of the pools; dense: batch /
+    // kv head / token strides of k and v.
+    int64_t k_stride0, k_stride1, k_stride2;
+    int64_t v_stride0, v_stride1, v_stride2;
+    int64_t num_blocks;
+    const int32_t* cu_seqlens;  // paged only
+    const int32_t* tables;      // paged only
+    int64_t table_stride;
+    int num_pages_per_seq;
+    const int32_t* kv_lens;    // paged only
+    const int32_t* positions;  // paged only (causal)
+    int num_seqs;              // paged: sequences; dense: batch
+    int q_len, kv_len;         // dense only
+    int n_heads, n_kv_heads, n_rep, head_groups;
+    int tiles_per_group;  // work items per (kv head, head group)
+    int total_work;       // tiles_per_group * n_kv_heads * head_groups
+    float scale_log2;
+};
+
+hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st);
+hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st);
+
+}  // namespace femto

@@ -1,0 +1,241 @@
+"""The reference's ``femtovllm._C`` extension surface, backed by libfemto_attn.so.
+
+Same names, attributes and argument meaning as the pybind11 module of the
+reference (csrc/bindings.cpp:35-98):
+
+* ``PagedAttentionGemvCuda(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len)``
+* ``PagedAttentionGemmCuda(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tables, kv_lens, positions)``
+* ``FlashAttentionWarpCuda(q, k, v)``
+* ``kMaxKVLenNonSplit``, ``kKVLenPerPage``, ``kDimHead``
+
+The functions run hand-written HIP kernels for gfx950 through the library's
+C ABI (include/femto_attn.h) on torch's current stream.  Argument checks
+raise ``RuntimeError`` where the reference's ``TORCH_CHECK``s do
+(csrc/paged_attention/paged_attention_gemv.cu:231-274,
+csrc/paged_attention/paged_attention_gemm.cu:314-353,
+csrc/flash_attention/flash_attention_warp.cu:306-349).  Importing this module
+raises ``ImportError`` when the library has not been built, exactly as the
+reference fails without its compiled extension (femtovllm/ops/__init__.py:6-16).
+
+Differences from the reference, all supersets: f32 decode is accepted (the
+reference dispatches f16/bf16 only), and the decode kernel splits long
+contexts internally, so ``max_kv_len`` only sizes the split workspace (the
+``kMaxKVLenNonSplit`` check is kept for API parity).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libfemto_attn.so")
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(_LIB_PATH):
+        raise ImportError(
+            "femtovllm HIP backend is not built: missing "
+            f"{_LIB_PATH}\nBuild it with: python nano-vllm-practice_amd/build.py"
+        )
+    lib = ctypes.CDLL(_LIB_PATH)
+    i, i64, p, sz = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+    lib.femto_attn_last_error.restype = ctypes.c_char_p
+    lib.femto_attn_last_error.argtypes = []
+    for name in ("femto_attn_max_kv_len_non_split", "femto_attn_kv_len_per_page", "femto_attn_dim_head"):
+        getattr(lib, name).restype = i
+        getattr(lib, name).argtypes = []
+    lib.femto_paged_attention_gemv_workspace_size.restype = sz
+    lib.femto_paged_attention_gemv_workspace_size.argtypes = [i, i, i]
+    lib.femto_paged_attention_gemv.restype = i
+    lib.femto_paged_attention_gemv.argtypes = [
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i64, p, i, i, i, p, sz, p,
+    ]
+    lib.femto_paged_attention_gemm.restype = i
+    lib.femto_paged_attention_gemm.argtypes = [
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p,
+    ]
+    lib.femto_flash_attention.restype = i
+    lib.femto_flash_attention.argtypes = [
+        i, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, i, i, i, i, i, i, p,
+    ]
+    return lib
+
+
+_lib = _load()
+
+kMaxKVLenNonSplit = int(_lib.femto_attn_max_kv_len_non_split())
+kKVLenPerPage = int(_lib.femto_attn_kv_len_per_page())
+kDimHead = int(_lib.femto_attn_dim_head())
+
+LIBRARY_PATH = _LIB_PATH
+
+_DTYPE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+_DTYPE_NAME = {torch.float32: "Float", torch.float16: "Half", torch.bfloat16: "BFloat16"}
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _raise_on(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(_lib.femto_attn_last_error().decode())
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dtype_code(t: torch.Tensor, fn: str) -> int:
+    code = _DTYPE.get(t.dtype)
+    _check(code is not None, f'"{fn}" not implemented for \'{t.dtype}\'')
+    return code
+
+
+# Split-KV workspaces, one per (device, stream): zero-filled once, the
+# kernel leaves its counters at zero after every call.
+_workspaces: dict = {}
+
+
+def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_len: int):
+    nbytes = int(_lib.femto_paged_attention_gemv_workspace_size(num_seqs, n_heads, max_kv_len))
+    if nbytes == 0:
+        return None, 0
+    key = (device.index, _stream(device))
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes + 256, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    ptr = ws.data_ptr()
+    aligned = (ptr + 255) & ~255
+    return aligned, ws.numel() - (aligned - ptr)
+
+
+def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q):
+    for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
+    if require_contiguous_q:
+        _check(q.is_contiguous(), f"{fn}: q must be contiguous")
+    _check(k_pool.is_contiguous() and v_pool.is_contiguous(), f"{fn}: k_pool and v_pool must be contiguous")
+    _check(q.dim() == 3, f"{fn}: q must be 3-D (n_heads, tokens, head_dim), got {q.dim()}-D")
+    _check(k_pool.dim() == 4 and v_pool.dim() == 4, f"{fn}: pools must be 4-D (num_blocks, n_kv_heads, 16, head_dim)")
+    _check(q.size(-1) == k_pool.size(-1) and q.size(-1) == v_pool.size(-1), f"{fn}: head_dim of q and pools differ")
+    _check(tuple(k_pool.shape) == tuple(v_pool.shape), f"{fn}: k_pool and v_pool shapes differ")
+    _check(q.dtype == k_pool.dtype == v_pool.dtype, f"{fn}: q, k_pool and v_pool must share a dtype")
+    _check(q.stride(-1) == 1, f"{fn}: q must be contiguous in head_dim")
+    _check(tables.dtype == torch.int32, f"{fn}: kv_page_tables must be int32")
+    _check(kv_lens.dtype == torch.int32, f"{fn}: kv_lens must be int32")
+    _check(tables.dim() == 2 and (tables.size(1) <= 1 or tables.stride(1) == 1), f"{fn}: kv_page_tables must be 2-D, row-major")
+    _check(kv_lens.is_contiguous(), f"{fn}: kv_lens must be contiguous")
+    for name, t in (("kv_page_tables", tables), ("kv_lens", kv_lens)):
+        _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
+    _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}, got {k_pool.size(2)}")
+    _check(q.size(-1) <= kDimHead, f"{fn}: head_dim must be <= {kDimHead}")
+    _check(q.size(0) % k_pool.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
+
+
+def _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len, require_contiguous_q=True):
+    fn = "PagedAttentionGemvCuda"
+    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q)
+    n_heads, num_seqs, dim = q.shape
+    _check(num_seqs == kv_page_tables.size(0), f"{fn}: q.size(1) must equal kv_page_tables.size(0)")
+    _check(num_seqs == kv_lens.size(0), f"{fn}: q.size(1) must equal kv_lens.size(0)")
+    _check(int(max_kv_len) <= kMaxKVLenNonSplit, f"{fn}: max_kv_len {max_kv_len} > kMaxKVLenNonSplit {kMaxKVLenNonSplit}")
+    dtype = _dtype_code(q, fn)
+    out = torch.empty((n_heads, num_seqs, dim), dtype=q.dtype, device=q.device)
+    if num_seqs == 0:
+        return out
+    ws, ws_bytes = _decode_workspace(q.device, num_seqs, n_heads, int(max_kv_len))
+    rc = _lib.femto_paged_attention_gemv(
+        dtype,
+        q.data_ptr(), q.stride(0), q.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(),
+        k_pool.size(0), k_pool.size(1), k_pool.size(2), k_pool.size(3),
+        k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
+        kv_lens.data_ptr(), num_seqs, n_heads, int(max_kv_len),
+        ws, ws_bytes,
+        _stream(q.device),
+    )
+    _raise_on(rc)
+    return out
+
+
+def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tables, kv_lens, positions,
+                          require_contiguous_q=True):
+    fn = "PagedAttentionGemmCuda"
+    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q)
+    for name, t in (("cu_seqlens", cu_seqlens), ("positions", positions)):
+        _check(t.dtype == torch.int32, f"{fn}: {name} must be int32")
+        _check(t.is_contiguous(), f"{fn}: {name} must be contiguous")
+        _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
+    num_seqs = cu_seqlens.numel() - 1
+    _check(num_seqs == kv_page_tables.size(0), f"{fn}: cu_seqlens.numel()-1 must equal kv_page_tables.size(0)")
+    _check(num_seqs == kv_lens.size(0), f"{fn}: cu_seqlens.numel()-1 must equal kv_lens.size(0)")
+    n_heads, num_tokens, dim = q.shape
+    _check(num_tokens == positions.numel(), f"{fn}: q.size(1) must equal positions.numel()")
+    _check(q.dtype != torch.float32, f'"{fn}" not implemented for \'Float\'')
+    dtype = _dtype_code(q, fn)
+    out = torch.empty((n_heads, num_tokens, dim), dtype=q.dtype, device=q.device)
+    if num_seqs <= 0 or num_tokens == 0:
+        return out
+    rc = _lib.femto_paged_attention_gemm(
+        dtype,
+        q.data_ptr(), q.stride(0), q.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(),
+        k_pool.size(0), k_pool.size(1), k_pool.size(2), k_pool.size(3),
+        k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        cu_seqlens.data_ptr(), num_seqs, num_tokens, n_heads,
+        kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
+        kv_lens.data_ptr(), positions.data_ptr(),
+        _stream(q.device),
+    )
+    _raise_on(rc)
+    return out
+
+
+def PagedAttentionGemvCuda(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len):
+    """Decode attention; out (n_heads, num_seqs, head_dim) like ``torch.empty_like(q)``."""
+    return _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len)
+
+
+def PagedAttentionGemmCuda(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tables, kv_lens, positions):
+    """Varlen causal prefill; out (n_heads, num_tokens, head_dim)."""
+    return _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tables, kv_lens, positions)
+
+
+def FlashAttentionWarpCuda(q, k, v):
+    """Dense non-causal GQA attention, q (B, H, Tq, 128), k/v (B, KVH, Tkv, 128)."""
+    fn = "FlashAttentionWarpCuda"
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
+        _check(t.is_contiguous(), f"{fn}: {name} must be contiguous")
+        _check(t.data_ptr() % 16 == 0, f"{fn}: {name} must be 16-byte aligned")
+        _check(t.dim() == 4, f"{fn}: {name} must be 4-D")
+    _check(q.size(0) == k.size(0) == v.size(0), f"{fn}: batch sizes differ")
+    _check(k.size(1) == v.size(1), f"{fn}: k and v head counts differ")
+    _check(q.size(1) % k.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
+    _check(k.size(2) == v.size(2), f"{fn}: k and v lengths differ")
+    _check(q.size(3) == k.size(3) == v.size(3), f"{fn}: head_dim differs")
+    _check(q.size(3) == kDimHead, f"{fn}: head_dim must be {kDimHead}")
+    _check(q.dtype == k.dtype == v.dtype, f"{fn}: q, k and v must share a dtype")
+    _check(q.dtype != torch.float32, f'"{fn}" not implemented for \'Float\'')
+    dtype = _dtype_code(q, fn)
+    out = torch.empty_like(q)
+    B, H, Tq, D = q.shape
+    rc = _lib.femto_flash_attention(
+        dtype,
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        B, H, k.size(1), Tq, k.size(2), D,
+        _stream(q.device),
+    )
+    _raise_on(rc)
+    return out

@@ -1,0 +1,106 @@
+"""Host-side varlen metadata, built the way the reference's ModelRunner builds it.
+
+``build_varlen_metadata`` reproduces femtovllm/engine/model_runner.py:187-202
+(prefill route) and 283-293 (decode route); ``pad_block_tables`` reproduces
+model_runner.py:46-72 (tables padded with -1, not 0).  The tensors it returns
+are exactly what ``femtovllm.ops.paged_attention_gemm`` /
+``paged_attention_gemv`` receive from the engine.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import torch
+
+
+@dataclasses.dataclass
+class VarlenMetadata:
+    """The attention fields of the reference's VarlenAttnMetadata (protocol.py:58-81)."""
+
+    positions: torch.Tensor
+    raw_positions: list
+    cu_seqlens: torch.Tensor
+    raw_cu_seqlens: list
+    max_q_len: int
+    Q_TILE_SIZE: int
+    cu_q_tiles: torch.Tensor
+    raw_cu_q_tiles: list
+    q_tile_to_seq_idx: torch.Tensor
+    raw_q_tile_to_seq_idx: list
+    kv_lens: torch.Tensor
+    raw_kv_lens: list
+    max_kv_len: int
+    block_tables: torch.Tensor
+    raw_block_tables: list
+
+    def to(self, device) -> "VarlenMetadata":
+        out = dataclasses.replace(self)
+        for f in dataclasses.fields(self):
+            v = getattr(self, f.name)
+            if isinstance(v, torch.Tensor):
+                setattr(out, f.name, v.to(device))
+        return out
+
+
+def pad_block_tables(raw_block_tables: list) -> list:
+    """Pad every table to the longest with -1 (model_runner.py:54-66)."""
+    if not raw_block_tables:
+        return []
+    width = max(len(t) for t in raw_block_tables)
+    return [list(t) + [-1] * (width - len(t)) for t in raw_block_tables]
+
+
+def build_varlen_metadata(
+    chunks: list,
+    raw_block_tables: list,
+    Q_TILE_SIZE: int = 32,
+    device: str | torch.device = "cpu",
+) -> VarlenMetadata:
+    """Metadata for one prefill (or unified) call.
+
+    ``chunks`` holds ``(num_computed_tokens, num_tokens)`` per scheduled
+    sequence.  As in model_runner.py:187-202: ``kv_len = pos + num_tokens``,
+    ``positions = range(pos, kv_len)``, ``ceil(num_tokens / Q_TILE_SIZE)``
+    query tiles per sequence.  A decode sequence is the chunk ``(L - 1, 1)``
+    (model_runner.py:283-289).
+    """
+    raw_positions: list = []
+    raw_cu_seqlens = [0]
+    raw_cu_q_tiles = [0]
+    raw_q_tile_to_seq_idx: list = []
+    raw_kv_lens: list = []
+    max_q_len = -1
+    max_kv_len = -1
+    for seq_idx, (pos, num_tokens) in enumerate(chunks):
+        kv_len = pos + num_tokens
+        raw_positions.extend(range(pos, kv_len))
+        raw_cu_seqlens.append(raw_cu_seqlens[-1] + num_tokens)
+        num_q_tiles = (num_tokens + Q_TILE_SIZE - 1) // Q_TILE_SIZE
+        raw_cu_q_tiles.append(raw_cu_q_tiles[-1] + num_q_tiles)
+        raw_q_tile_to_seq_idx.extend([seq_idx] * num_q_tiles)
+        raw_kv_lens.append(kv_len)
+        max_q_len = max(max_q_len, num_tokens)
+        max_kv_len = max(max_kv_len, kv_len)
+
+    def i32(x):
+        return torch.tensor(x, dtype=torch.int32, device=device)
+
+    padded = pad_block_tables(raw_block_tables)
+    return VarlenMetadata(
+        positions=i32(raw_positions),
+        raw_positions=raw_positions,
+        cu_seqlens=i32(raw_cu_seqlens),
+        raw_cu_seqlens=raw_cu_seqlens,
+        max_q_len=max_q_len,
+        Q_TILE_SIZE=Q_TILE_SIZE,
+        cu_q_tiles=i32(raw_cu_q_tiles),
+        raw_cu_q_tiles=raw_cu_q_tiles,
+        q_tile_to_seq_idx=i32(raw_q_tile_to_seq_idx),
+        raw_q_tile_to_seq_idx=raw_q_tile_to_seq_idx,
+        kv_lens=i32(raw_kv_lens),
+        raw_kv_lens=raw_kv_lens,
+        max_kv_len=max_kv_len,
+        block_tables=torch.tensor(padded, dtype=torch.int32, device=device).reshape(len(padded), -1),
+        raw_block_tables=[list(t) for t in raw_block_tables],
+    )

@@ -1,0 +1,132 @@
+"""Attention operators with the reference's call signatures.
+
+``paged_attention_gemv`` and ``paged_attention_gemm`` keep the signatures,
+defaults, constants and error behaviour of femtovllm/ops/__init__.py:21-156
+of the reference, so the engine, scheduler, prefix tree and block tables
+drive them unchanged.  Both run hand-written HIP kernels for gfx950
+(``libfemto_attn.so`` through :mod:`femtovllm._C`); importing this module
+raises ``ImportError`` when that library is missing (ops/__init__.py:6-16).
+
+``impl`` is kept for signature compatibility: ``ImplCustomKernel.CUDA`` and,
+for the prefill op, ``ImplCustomKernel.TRITON`` (the reference's default)
+both select the HIP kernels; anything else raises ``NotImplementedError``
+as in the reference (ops/__init__.py:106-107, 155-156).
+
+One deliberate difference: ``q`` arrives as ``q.transpose(0, 1)`` of a
+``(tokens, n_heads, head_dim)`` tensor (femtovllm/models/qwen/qwen3.py:270,
+372).  The reference copies it with ``.contiguous()``; the HIP kernels take
+the head and token strides directly, so no copy is made as long as the
+head dimension is contiguous.
+"""
+
+import torch
+
+import femtovllm
+from femtovllm.protocol import ImplCustomKernel
+
+try:
+    from femtovllm import _C as _hip_backend
+except ImportError as e:
+    raise ImportError(
+        "Failed to load the femtovllm HIP backend (libfemto_attn.so).\n"
+        "Build it for gfx950 with:\n"
+        "    python nano-vllm-practice_amd/build.py"
+    ) from e
+
+MAX_KV_LEN_NON_SPLIT = _hip_backend.kMaxKVLenNonSplit
+
+KV_LEN_PER_PAGE = _hip_backend.kKVLenPerPage
+# The kernels are built for this exact head dim (register tiling), as in the
+# reference (femtovllm/ops/__init__.py:24-26).
+DIM_HEAD = _hip_backend.kDimHead
+
+
+def _ensure_valid_tensor(t: torch.Tensor, name: str) -> torch.Tensor:
+    """Require a GPU tensor (ValueError otherwise, ops/__init__.py:36-39).
+
+    Strided views are passed through; only a tensor whose innermost
+    dimension is not contiguous is copied.
+    """
+    if not t.is_cuda:
+        raise ValueError(f"Argument '{name}' must be a CUDA tensor. Got device={t.device}")
+    if t.stride(-1) != 1:
+        return t.contiguous()
+    return t
+
+
+def paged_attention_gemv(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    kv_page_tables: torch.Tensor,
+    kv_lens: torch.Tensor,
+    max_kv_len: int,
+    #####
+    impl: ImplCustomKernel = None,
+):
+    """Decode attention over the paged KV cache.
+
+    q (n_heads, num_seqs, head_dim); pools (num_blocks, n_kv_heads, 16,
+    head_dim); kv_page_tables (num_seqs, max_pages) int32, -1 padded;
+    kv_lens (num_seqs,) int32.  Returns (n_heads, num_seqs, head_dim).
+    """
+    q = _ensure_valid_tensor(q, "q")
+
+    impl = femtovllm._DEV.impl_custom_gemv if (impl is None) else impl
+
+    if impl == ImplCustomKernel.CUDA:
+        return _hip_backend._paged_attention_gemv(
+            q,
+            k_pool,
+            v_pool,
+            kv_page_tables,
+            kv_lens,
+            max_kv_len,
+            require_contiguous_q=False,
+        )
+    else:
+        raise NotImplementedError()
+
+
+def paged_attention_gemm(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_q_len: int,
+    Q_TILE_SIZE: int,
+    cu_q_tiles: torch.Tensor,
+    q_tile_to_seq_idx: torch.Tensor,
+    kv_page_tables: torch.Tensor,
+    kv_lens: torch.Tensor,
+    positions: torch.Tensor,
+    #####
+    impl: ImplCustomKernel = None,
+):
+    """Chunked / varlen / causal prefill over the paged KV cache.
+
+    q (n_heads, num_tokens, head_dim) with sequences delimited by
+    cu_seqlens; token t sees key j iff j < kv_lens[seq] and
+    j <= positions[t].  ``Q_TILE_SIZE``, ``cu_q_tiles`` and
+    ``q_tile_to_seq_idx`` describe the reference Triton kernel's launch grid;
+    the HIP kernel derives its own tiles from ``cu_seqlens`` and ignores them.
+    Returns (n_heads, num_tokens, head_dim).
+    """
+    q = _ensure_valid_tensor(q, "q")
+
+    impl = femtovllm._DEV.impl_custom_gemm if (impl is None) else impl
+
+    if impl == ImplCustomKernel.CUDA or impl == ImplCustomKernel.TRITON:
+        return _hip_backend._paged_attention_gemm(
+            q,
+            k_pool,
+            v_pool,
+            cu_seqlens,
+            max_q_len,
+            kv_page_tables,
+            kv_lens,
+            positions,
+            require_contiguous_q=False,
+        )
+    else:
+        raise NotImplementedError()

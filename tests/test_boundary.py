@@ -1,0 +1,157 @@
+"""CPU tests of the drop-in boundary: the C ABI library and the Python mirror.
+
+No GPU work is launched here: every C-ABI call below fails argument
+validation before any HIP call, and tensor-level checks run on CPU tensors.
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "femto_attn.h")
+
+
+@pytest.fixture(scope="module")
+def C():
+    from femtovllm import _C
+
+    return _C
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(femto_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(C):
+    declared = header_functions()
+    assert "femto_paged_attention_gemv" in declared and "femto_paged_attention_gemm" in declared
+    nm = subprocess.run(["nm", "-D", "--defined-only", C.LIBRARY_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT\s+(femto_\w+)", nm.stdout))
+    missing = [f for f in declared if f not in exported]
+    assert not missing, f"declared in femto_attn.h but not exported: {missing}"
+    lib = ctypes.CDLL(C.LIBRARY_PATH)
+    for f in declared:
+        getattr(lib, f)
+
+
+def test_library_is_built_for_gfx950(C):
+    out = subprocess.run(["strings", C.LIBRARY_PATH], capture_output=True, text=True).stdout
+    assert "gfx950" in out
+
+
+def test_constants_match_reference(C):
+    # csrc/utils/constants.cuh:8, 39, 75 via csrc/bindings.cpp:62-66
+    assert C.kMaxKVLenNonSplit == 8192
+    assert C.kKVLenPerPage == 16
+    assert C.kDimHead == 128
+    from femtovllm import ops
+
+    assert (ops.MAX_KV_LEN_NON_SPLIT, ops.KV_LEN_PER_PAGE, ops.DIM_HEAD) == (8192, 16, 128)
+
+
+def test_workspace_size(C):
+    f = C._lib.femto_paged_attention_gemv_workspace_size
+    assert f(0, 16, 4096) == 0
+    small = f(4, 16, 17)
+    big = f(64, 16, 4096)
+    assert big > small >= 0
+    assert big % 4 == 0
+
+
+def _gemv(C, **kw):
+    a = dict(dtype=2, q=16, qsh=128, qsb=2048, out=16, osh=128, osb=2048, k=16, v=16, nb=8, kvh=8, bs=16, d=128,
+             ps0=16384, ps1=2048, ps2=128, tables=16, npages=4, ts=4, kv_lens=16, nseq=4, h=16, maxkv=64,
+             ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return C._lib.femto_paged_attention_gemv(*a.values())
+
+
+def test_gemv_validation_errors(C):
+    last = lambda: C._lib.femto_attn_last_error().decode()
+    assert _gemv(C, d=64) == 2 and "head_dim must be 128" in last()
+    assert _gemv(C, bs=32) == 1 and "block_size must be 16" in last()
+    assert _gemv(C, h=12) == 1 and "multiple of n_kv_heads" in last()
+    assert _gemv(C, dtype=7) == 2
+    assert _gemv(C, q=8) == 1 and "aligned" in last()
+    assert _gemv(C, ps2=100) == 1 and "strides" in last()
+    assert _gemv(C, nseq=0) == 0  # nothing to do
+    # a multi-split plan without a workspace is rejected before launch
+    assert _gemv(C, maxkv=8192, nseq=64) == 1 and "workspace" in last()
+
+
+def test_gemm_rejects_fp32(C):
+    rc = C._lib.femto_paged_attention_gemm(0, 16, 128, 128, 16, 128, 128, 16, 16, 8, 8, 16, 128, 16384, 2048, 128,
+                                           16, 2, 10, 16, 16, 4, 4, 16, 16, None)
+    assert rc == 2
+    assert "not implemented for 'Float'" in C._lib.femto_attn_last_error().decode()
+
+
+def test_flash_validation(C):
+    rc = C._lib.femto_flash_attention(2, 16, 1, 1, 1, 16, 1, 1, 1, 16, 1, 1, 1, 16, 4, 4, 4, 1, 4, 4, 8, 8, 128, None)
+    assert rc == 1 and "strides" in C._lib.femto_attn_last_error().decode()
+    rc = C._lib.femto_flash_attention(2, 16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, 1, 4, 4, 8, 8, 64, None)
+    assert rc == 2
+
+
+def test_ops_reject_cpu_tensors():
+    from femtovllm import ops
+
+    q = torch.zeros(16, 2, 128, dtype=torch.bfloat16)
+    pool = torch.zeros(4, 8, 16, 128, dtype=torch.bfloat16)
+    t = torch.zeros(2, 1, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        ops.paged_attention_gemv(q, pool, pool, t, t[:, 0], 16)
+    with pytest.raises(ValueError):
+        ops.paged_attention_gemm(q, pool, pool, t[:, 0], 1, 32, t[:, 0], t[:, 0], t, t[:, 0], t[:, 0])
+
+
+def test_dev_flags_and_enums_mirror_reference():
+    import femtovllm
+    from femtovllm.protocol import AttentionBackend, ImplCustomKernel
+
+    assert femtovllm._DEV.impl_custom_gemm == ImplCustomKernel.TRITON
+    assert femtovllm._DEV.impl_custom_gemv == ImplCustomKernel.CUDA
+    assert femtovllm._DEV.route_prefill_decode
+    assert AttentionBackend("custom_gemm_gemv") is AttentionBackend.CUSTOM_GEMM_GEMV
+    assert ImplCustomKernel("cuda") is ImplCustomKernel.CUDA
+
+
+def test_metadata_follows_model_runner():
+    """femtovllm/engine/model_runner.py:187-202 on the reference test's layout."""
+    from femtovllm.metadata import build_varlen_metadata
+
+    m = build_varlen_metadata([(51, 8), (28, 16)], [[0, 4, 5, 6], [1, 8, 9]], Q_TILE_SIZE=16)
+    assert m.raw_cu_seqlens == [0, 8, 24]
+    assert m.raw_kv_lens == [59, 44]
+    assert m.raw_positions == list(range(51, 59)) + list(range(28, 44))
+    assert m.raw_cu_q_tiles == [0, 1, 2]
+    assert m.raw_q_tile_to_seq_idx == [0, 1]
+    assert m.block_tables.tolist() == [[0, 4, 5, 6], [1, 8, 9, -1]]
+    assert m.max_q_len == 16 and m.max_kv_len == 59
+
+
+def test_workloads_follow_generation_rules():
+    import numpy as np
+
+    from femtovllm import workloads
+
+    w = workloads.decode_fp32_small()
+    assert [p + n for p, n in w.chunks] == [17, 64, 200, 511]
+    assert w.k_pool.shape == (256, 8, 16, 128) and w.q.shape == (16, 4, 128)
+    used = sorted(b for t in w.raw_block_tables for b in t)
+    assert len(used) == len(set(used)) == sum(-(-L // 16) for L in (17, 64, 200, 511))
+    unused = sorted(set(range(256)) - set(used))
+    assert torch.isnan(w.k_pool[unused]).all()
+    # tail rows of a last page are poisoned, visible rows are finite
+    t0 = w.raw_block_tables[0]
+    assert torch.isnan(w.k_pool[t0[-1], :, 1:]).all() and torch.isfinite(w.k_pool[t0[-1], :, :1]).all()
+    assert workloads.prefill_flops([(0, 2048)], 32, 128) == 4 * 128 * 32 * (2048 * 2049 // 2)
+    b = workloads.decode_bytes(w, unique_blocks=False)
+    assert b == (17 + 64 + 200 + 511) * 8 * 128 * 4 * 2 + 2 * 16 * 4 * 128 * 4 + 4 * 51 + 16

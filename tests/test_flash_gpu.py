@@ -1,0 +1,79 @@
+"""Parity of the dense flash-attention entry (femto_flash_attention) with the oracle.
+
+Reference behaviour: FlashAttentionWarpCuda
+(csrc/flash_attention/flash_attention_warp.cu:301-376): dense, non-causal,
+GQA, q (B, H, Tq, 128), k/v (B, KVH, Tkv, 128).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as oa
+from femtovllm import workloads
+from helpers import assert_close, np64
+
+pytestmark = pytest.mark.gpu
+
+
+def rand(shape, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+@pytest.fixture(scope="module")
+def C(gpu):
+    from femtovllm import _C
+
+    return _C
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (4, 2, 2, 64, 64),     # csrc/flash_attention/test_flash_attention.py:9-18
+        (2, 4, 4, 16, 16),     # benchmarks/flash_attention/scripts/benchmark.py:56-57
+        (2, 4, 4, 256, 256),
+        (2, 8, 2, 100, 333),   # GQA, ragged lengths
+        (1, 32, 8, 129, 1),
+        (3, 6, 6, 1, 77),
+    ],
+)
+def test_dense_attention(C, gpu, dtype, shape):
+    B, H, KVH, Tq, Tkv = shape
+    q = rand((B, H, Tq, 128), dtype, 1)
+    k = rand((B, KVH, Tkv, 128), dtype, 2)
+    v = rand((B, KVH, Tkv, 128), dtype, 3)
+    out = C.FlashAttentionWarpCuda(q.to(gpu), k.to(gpu), v.to(gpu))
+    torch.cuda.synchronize()
+    want = oa.dense_attention(np64(q), np64(k), np64(v))
+    assert_close(out, want, dtype, f"dense {shape} {dtype}")
+
+
+def test_dense_equals_paged_identity_table(C, ops, gpu):
+    """Dense attention == paged prefill with contiguous pages and no causal limit."""
+    B, H, KVH, T = 1, 8, 4, 96
+    q = rand((B, H, T, 128), torch.bfloat16, 4)
+    k = rand((B, KVH, T, 128), torch.bfloat16, 5)
+    v = rand((B, KVH, T, 128), torch.bfloat16, 6)
+    dense = C.FlashAttentionWarpCuda(q.to(gpu), k.to(gpu), v.to(gpu))
+    k_pool = k[0].reshape(KVH, T // 16, 16, 128).transpose(0, 1).contiguous().to(gpu)
+    v_pool = v[0].reshape(KVH, T // 16, 16, 128).transpose(0, 1).contiguous().to(gpu)
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=gpu)
+    paged = ops.paged_attention_gemm(
+        q[0].to(gpu), k_pool, v_pool, i32([0, T]), T, 32, i32([0, 3]), i32([0, 0, 0]),
+        i32([list(range(T // 16))]), i32([T]), i32([T - 1] * T),
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(dense[0], paged)
+
+
+def test_dense_errors(C, gpu):
+    q = rand((1, 2, 8, 128), torch.bfloat16, 7).to(gpu)
+    with pytest.raises(RuntimeError):
+        C.FlashAttentionWarpCuda(q, q[:, :1, :5], q[:, :1, :5])  # k / v not contiguous
+    with pytest.raises(RuntimeError):
+        C.FlashAttentionWarpCuda(q.float(), q.float(), q.float())
+    with pytest.raises(RuntimeError):
+        C.FlashAttentionWarpCuda(q[..., :64].contiguous(), q[..., :64].contiguous(), q[..., :64].contiguous())

@@ -1,0 +1,186 @@
+"""Parity of the HIP MFMA prefill kernel (femto_paged_attention_gemm) with the oracle.
+
+Reference behaviour: paged_attention_gemm_triton
+(femtovllm/ops/triton/paged_attention/paged_attention_gemm.py:165-235) and
+PagedAttentionGemmCuda (csrc/paged_attention/paged_attention_gemm.cu:304-395)
+behind femtovllm.ops.paged_attention_gemm (femtovllm/ops/__init__.py:110-156).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as oa
+from femtovllm import workloads
+from femtovllm.metadata import build_varlen_metadata
+from helpers import assert_close, np32, np64, np_tables, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gemm(ops, q, meta, k_pool, v_pool, device, impl=None):
+    out = ops.paged_attention_gemm(
+        q.to(device), k_pool, v_pool, meta.cu_seqlens, meta.max_q_len, meta.Q_TILE_SIZE, meta.cu_q_tiles,
+        meta.q_tile_to_seq_idx, meta.block_tables, meta.kv_lens, meta.positions, impl=impl,
+    )
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle_prefill(q, meta, k_pool, v_pool, rows=None):
+    return oa.paged_prefill(np64(q), np32(k_pool), np32(v_pool), meta.raw_cu_seqlens, np_tables(meta),
+                            meta.raw_kv_lens, np.asarray(meta.raw_positions), rows=rows)
+
+
+def check_workload(ops, w, gpu, seqs=None, rows_per_seq=None, what=""):
+    q, meta = w.gemm_call(seqs=seqs, device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    rows = None
+    if rows_per_seq is not None:
+        rows = sample_rows(meta.raw_cu_seqlens, rows_per_seq, np.random.default_rng(0))
+    want = oracle_prefill(q, meta, w.k_pool, w.v_pool, rows=rows)
+    mask = None
+    if rows is not None:
+        mask = np.zeros(want.shape, dtype=bool)
+        mask[:, rows] = True
+    return assert_close(out, want, w.dtype, what, mask=mask)
+
+
+def test_reference_fixture_structure(ops, gpu):
+    """cu_seqlens [0,8,24], kv_lens [59,44], tables [[0,4,5,6],[1,8,9,-1]], H=8, KVH=4."""
+    w = workloads.reference_fixture()
+    err = check_workload(ops, w, gpu, what="reference fixture")
+    print(f"reference fixture max abs err {err:.2e}")
+
+
+@pytest.mark.parametrize("impl", ["cuda", "triton"])
+def test_impl_flag_routes_to_hip(ops, gpu, impl):
+    from femtovllm.protocol import ImplCustomKernel
+
+    w = workloads.reference_fixture()
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu, impl=ImplCustomKernel(impl))
+    assert_close(out, oracle_prefill(q, meta, w.k_pool, w.v_pool), torch.bfloat16, impl)
+
+
+def test_chunked_prefill_8x512(ops, gpu):
+    w = workloads.prefill_bf16_chunked()
+    err = check_workload(ops, w, gpu, rows_per_seq=48, what="8x512 chunked prefill")
+    print(f"8x512 max abs err {err:.2e}")
+
+
+@pytest.mark.parametrize("chunk", [0, 7, 15])
+def test_long_context_chunks(ops, gpu, chunk):
+    w = workloads.prefill_bf16_long_llama3_8b()
+    q, meta = workloads.long_context_chunk(w, chunk, device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    rows = sample_rows(meta.raw_cu_seqlens, 24, np.random.default_rng(chunk))
+    want = oracle_prefill(q, meta, w.k_pool, w.v_pool, rows=rows)
+    mask = np.zeros(want.shape, dtype=bool)
+    mask[:, rows] = True
+    assert_close(out, want, torch.bfloat16, f"long-context chunk {chunk}", mask=mask)
+
+
+def test_mixed_batch_single_call(ops, gpu):
+    """One 1024-token chunk on a 4096 prefix plus 127 decode rows in one call, shared blocks."""
+    w = workloads.mixed_bf16_qwen3_8b()
+    check_workload(ops, w, gpu, rows_per_seq=2, what="mixed batch")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads", [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (6, 1)])
+def test_prefill_gqa_and_dtypes(ops, gpu, dtype, heads):
+    H, KVH = heads
+    rng = np.random.default_rng(H * 7 + KVH)
+    chunks = [(int(rng.integers(0, 300)), int(rng.integers(1, 200))) for _ in range(4)] + [(0, 1), (31, 33)]
+    w = workloads.make_paged_workload("gqa", chunks, H, KVH, dtype=dtype, seed=H + 3 * KVH)
+    check_workload(ops, w, gpu, what=f"prefill H={H} KVH={KVH} {dtype}")
+
+
+def test_arbitrary_positions(ops, gpu):
+    """The mask comes from positions[], not from the chunk layout."""
+    w = workloads.make_paged_workload("pos", [(60, 40), (0, 70)], 16, 8, seed=21)
+    q, meta = w.gemm_call(device=gpu)
+    rng = np.random.default_rng(21)
+    pos = []
+    for (p, n) in w.chunks:
+        pos.extend(int(x) for x in rng.integers(0, p + n, size=n))
+    meta.positions = torch.tensor(pos, dtype=torch.int32, device=gpu)
+    meta.raw_positions = pos
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    assert_close(out, oracle_prefill(q, meta, w.k_pool, w.v_pool), torch.bfloat16, "arbitrary positions")
+
+
+def test_causal_boundary_spike_is_exact(ops, gpu):
+    """Key j = positions[t] is selected bit-exactly; key positions[t] + 1 is not.
+
+    Token i (position 50 + i) queries along its own dim i.  Even tokens get a
+    spike key at their own position, odd tokens one position later.
+    """
+    H, KVH = 2, 1
+    L, n = 150, 100
+    w = workloads.make_paged_workload("causal", [(L - n, n)], H, KVH, seed=22)
+    w.k_pool.zero_()
+    w.q.zero_()
+    table = w.raw_block_tables[0]
+    for i in range(n):
+        p = L - n + i + (i % 2)
+        w.q[:, i, i] = 3000.0
+        if p < L:
+            w.k_pool[table[p // 16], 0, p % 16, i] = 1.0
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu).cpu()
+    for i in range(0, n, 2):
+        p = L - n + i
+        want = w.v_pool[table[p // 16], 0, p % 16]
+        for h in range(H):
+            assert torch.equal(out[h, i], want), f"token {i}: key at its own position not selected exactly"
+    want = oracle_prefill(q, meta, w.k_pool, w.v_pool)
+    assert_close(out, want, torch.bfloat16, "causal boundary")
+
+
+def test_empty_sequences_and_kv_len_zero(ops, gpu):
+    """Zero-length chunks produce no rows; kv_len == 0 rows are NaN as in the reference."""
+    w = workloads.make_paged_workload("empty", [(10, 5), (20, 0), (0, 3)], 8, 4, seed=23)
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    assert_close(out, oracle_prefill(q, meta, w.k_pool, w.v_pool), torch.bfloat16, "empty seq")
+    kv0 = meta.kv_lens.clone()
+    kv0[2] = 0
+    out = ops.paged_attention_gemm(q.to(gpu), wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len, 32,
+                                   meta.cu_q_tiles, meta.q_tile_to_seq_idx, meta.block_tables, kv0, meta.positions)
+    torch.cuda.synchronize()
+    assert torch.isnan(out[:, 5:8].float()).all()
+    assert not torch.isnan(out[:, :5].float()).any()
+
+
+def test_one_token_chunk_equals_decode(ops, gpu):
+    w = workloads.make_paged_workload("dec", [(L - 1, 1) for L in (33, 700, 1500)], 16, 8, seed=24)
+    wd = w.to(gpu)
+    q, meta = w.gemm_call(device=gpu)
+    a = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    b = ops.paged_attention_gemv(q.to(gpu), wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens, meta.max_kv_len)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-2
+
+
+def test_strided_q_and_errors(ops, gpu):
+    w = workloads.make_paged_workload("st", [(30, 50)], 16, 8, seed=25)
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    strided = q.transpose(0, 1).contiguous().to(gpu).transpose(0, 1)
+    a = run_gemm(ops, strided, meta, wd.k_pool, wd.v_pool, gpu)
+    b = run_gemm(ops, strided.contiguous(), meta, wd.k_pool, wd.v_pool, gpu)
+    assert torch.equal(a, b)
+    with pytest.raises(ValueError):
+        run_gemm(ops, q.cpu(), meta, wd.k_pool, wd.v_pool, "cpu")
+    with pytest.raises(NotImplementedError):
+        run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu, impl="opencl")
+    with pytest.raises(RuntimeError):
+        qf = q.float().to(gpu)
+        run_gemm(ops, qf, meta, wd.k_pool.float(), wd.v_pool.float(), gpu)
