@@ -6,8 +6,8 @@
  * launches hand-written HIP kernels on the given stream (a hipStream_t
  * passed as void*, NULL = the null stream) and returns without
  * synchronising.  No entry point allocates device memory: outputs and the
- * decode workspace belong to the caller.  Inputs are read-only; the KV pools
- * are never written except by femto_paged_kv_cache_write.
+ * decode workspace belong to the caller.  Inputs, including the KV pools,
+ * are read-only.
  *
  * Return value: FEMTO_OK, or an error code with a message available from
  * femto_attn_last_error() (thread-local, valid until the next call on the
@@ -49,11 +49,11 @@ int femto_attn_max_kv_len_non_split(void);
 int femto_attn_kv_len_per_page(void);
 int femto_attn_dim_head(void);
 
-/* Bytes of workspace femto_paged_attention_gemv needs for these sizes.
- * The workspace must be zero-filled before its first use; every call
- * leaves its counter section zeroed again, so one buffer can be reused by
- * calls that are ordered on one stream (calls that overlap must not share
- * a workspace). */
+/* Bytes of workspace femto_paged_attention_gemv needs for these sizes
+ * (0 when no sequence is split).  It holds the per-split partial softmax
+ * states between the split kernel and the merge kernel of one call; no
+ * initialisation is needed.  Calls that may overlap (other streams) must
+ * not share a workspace. */
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len);
 
 /* Paged decode attention: one query token per sequence attends to all

@@ -76,13 +76,9 @@ DecodePlan plan_paged_decode(int num_seqs, int n_heads, int n_kv_heads, int max_
 }
 
 size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_splits) {
-    if (max_splits <= 1) return 0;
+    if (max_splits <= 1 || num_seqs <= 0) return 0;
     const size_t slots = (size_t)num_seqs * n_heads * max_splits;
-    size_t bytes = slots * kDimHead * sizeof(float);
-    bytes += slots * 2 * sizeof(float);
-    bytes = (bytes + 255) & ~size_t(255);
-    bytes += (size_t)num_seqs * n_heads * sizeof(int);
-    return bytes;
+    return slots * (kDimHead + 2) * sizeof(float);
 }
 
 }  // namespace femto
@@ -117,8 +113,8 @@ static int check_paged_common(const char* fn, int dtype, const void* q, const vo
         return fail(FEMTO_ERR_INVALID, f + ": n_heads (" + std::to_string(n_heads) +
                                            ") must be a positive multiple of n_kv_heads (" +
                                            std::to_string(n_kv_heads) + ")");
-    if (num_blocks < 0 || num_pages_per_seq < 0 || table_stride < 0)
-        return fail(FEMTO_ERR_INVALID, f + ": negative pool or table size");
+    if (num_blocks < 1 || num_pages_per_seq < 0 || table_stride < 0)
+        return fail(FEMTO_ERR_INVALID, f + ": the pool needs at least one block and table sizes must be >= 0");
     if (!q || !out || !k_pool || !v_pool || (num_pages_per_seq > 0 && !tables))
         return fail(FEMTO_ERR_INVALID, f + ": null pointer argument");
     const int vec = 16 / elem_bytes(dtype);
@@ -152,7 +148,7 @@ int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, 
     const size_t need = femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_splits);
     if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: workspace of " + std::to_string(need) +
-                                           " bytes (256-byte aligned, zero-filled before first use) required, got " +
+                                           " bytes (256-byte aligned) required, got " +
                                            std::to_string(workspace_bytes));
 
     femto::DecodeArgs a{};
@@ -179,13 +175,9 @@ int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, 
     a.max_splits = plan.max_splits;
     a.scale_log2 = scale_log2(head_dim);
     if (need > 0) {
-        char* ws = static_cast<char*>(workspace);
         const size_t slots = (size_t)num_seqs * n_heads * plan.max_splits;
-        a.part_acc = reinterpret_cast<float*>(ws);
-        a.part_ml = reinterpret_cast<float*>(ws + slots * femto::kDimHead * sizeof(float));
-        size_t coff = slots * (femto::kDimHead + 2) * sizeof(float);
-        coff = (coff + 255) & ~size_t(255);
-        a.counters = reinterpret_cast<int*>(ws + coff);
+        a.part_acc = static_cast<float*>(workspace);
+        a.part_ml = a.part_acc + slots * femto::kDimHead;
     }
     return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, plan.max_splits, num_seqs,
                                                  static_cast<hipStream_t>(stream)),

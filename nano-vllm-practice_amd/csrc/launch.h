@@ -26,7 +26,6 @@ struct DecodeArgs {
     float scale_log2;
     float* part_acc;  // [num_seqs][n_heads][max_splits][128]
     float* part_ml;   // [num_seqs][n_heads][max_splits][2]
-    int* counters;    // [num_seqs][n_heads / nrep_tile]
 };
 
 // Split size (pages per workgroup) and split count used for a decode call.

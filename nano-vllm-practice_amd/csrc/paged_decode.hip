@@ -13,13 +13,19 @@
 //    (16 lanes) owns page rows r, r+4, r+8, r+12 and lane c of the row owns 8
 //    head dims, so each K/V page is 4 coalesced 16-byte loads per lane
 //    (bf16/f16; f32 uses 8) and the q.k reduction stays inside a DPP row;
+//  * block ids are fetched 64 at a time (one per lane) and broadcast with
+//    readlane, and each wave keeps two pages of loads in flight, so the
+//    table never adds a dependent load per page;
 //  * every lane keeps an online-softmax state (max, sum, 8 accumulators) per
 //    query head over the keys it saw; states merge across DPP rows with
-//    shuffles, across waves through LDS and across splits through a
-//    workspace, the last workgroup of a (sequence, KV head) to finish doing
-//    the final merge (no second kernel launch);
-//  * rows past kv_len (and blocks outside the pool) are never loaded: the
-//    registers are zeroed, so NaN in unused pool memory cannot leak.
+//    shuffles and across waves through LDS; split sequences leave one
+//    partial state per split in the workspace and a small merge kernel on
+//    the same stream combines them (no cross-workgroup fences or atomics,
+//    which on gfx950 would write back and invalidate the XCD's L2);
+//  * rows past kv_len are never read (loads are clamped to the last visible
+//    row and their scores masked) and block ids outside the pool are never
+//    dereferenced (their page reads as zeros), so NaN in unused pool memory
+//    cannot leak.
 #include "common.h"
 #include "launch.h"
 
@@ -89,6 +95,12 @@ __device__ __forceinline__ void store_elem<F32>(char* base, int64_t idx, float v
 // while a lane has seen no visible key.
 constexpr float kEmptyMax = -1.0e30f;
 
+// K and V rows of one page held by a lane: page rows rg, rg+4, rg+8, rg+12.
+template <typename E>
+struct PageRegs {
+    RowSlice<E> k[4], v[4];
+};
+
 template <typename E, int NREP>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     constexpr int EB = E::kBytes;
@@ -144,35 +156,52 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
     }
 
+    // This wave owns pages p0 + wave + 4*i, i < n_mine.  Their block ids are
+    // fetched 64 at a time, one per lane, and broadcast with readlane.
+    const int n_mine = (p1 - p0 - wave + 3) >> 2;
     const int32_t* table = a.tables + (int64_t)b * a.table_stride;
     const char* kpool = reinterpret_cast<const char*>(a.k_pool);
     const char* vpool = reinterpret_cast<const char*>(a.v_pool);
     const int64_t head_off = (int64_t)kvh * a.pool_stride_head;
+    int tbl = -1;
 
-    for (int pg = p0 + wave; pg < p1; pg += 4) {
-        const int blk = pg < a.num_pages_per_seq ? table[pg] : -1;
-        const bool blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
-        const int64_t page_off = ((int64_t)blk * a.pool_stride_block + head_off) * EB;
-        RowSlice<E> kr[4], vr[4];
+    auto fetch_table = [&](int i0) {
+        const int pg = p0 + wave + 4 * (i0 + lane);
+        tbl = (i0 + lane < n_mine && pg < a.num_pages_per_seq) ? table[pg] : -1;
+    };
+    // Issue the 8 (f32: 16) 16-byte loads of page i.  Rows past kv_len are
+    // clamped to the last visible row and blocks outside the pool to block 0,
+    // so every load is in bounds and unconditional; those values are never
+    // used (masked scores, zeroed registers).
+    auto issue = [&](int i, PageRegs<E>& pr, bool& blk_ok) {
+        const int blk = __builtin_amdgcn_readlane(tbl, i & 63);
+        blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+        const int pg = p0 + wave + 4 * i;
+        const int last_row = kv_len - 1 - pg * kPage;
+        const int64_t page_off = ((int64_t)(blk_ok ? blk : 0) * a.pool_stride_block + head_off) * EB;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int row = rg + 4 * j;
-            const bool ok = blk_ok && (pg * kPage + row) < kv_len;
+            const int row = min(rg + 4 * j, last_row);
             const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
-            if (ok) {
-                kr[j].load(kpool + off, c);
-                vr[j].load(vpool + off, c);
-            } else {
-                kr[j].zero();
-                vr[j].zero();
+            pr.k[j].load(kpool + off, c);
+            pr.v[j].load(vpool + off, c);
+        }
+    };
+    auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
+        if (!blk_ok) {
+            // A block id outside the pool reads as a page of zeros.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pr.k[j].zero();
+                pr.v[j].zero();
             }
         }
-
+        const int pg = p0 + wave + 4 * i;
         float sc[NREP][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float kf[8];
-            kr[j].to_float(kf);
+            pr.k[j].to_float(kf);
 #pragma unroll
             for (int r = 0; r < NREP; ++r) {
                 float d = 0.0f;
@@ -190,11 +219,9 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
                 sc[r][j] = valid ? t : -INFINITY;
             }
         }
-
         float vf[4][8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vr[j].to_float(vf[j]);
-
+        for (int j = 0; j < 4; ++j) pr.v[j].to_float(vf[j]);
 #pragma unroll
         for (int r = 0; r < NREP; ++r) {
             const float mx = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
@@ -214,6 +241,28 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
                 acc[r][e] = t;
             }
             m[r] = mn;
+        }
+    };
+
+    // Two pages in flight per wave: page i+1 loads while page i computes.
+    PageRegs<E> ra, rb;
+    bool ok_a = false, ok_b = false;
+    if (n_mine > 0) {
+        fetch_table(0);
+        issue(0, ra, ok_a);
+    }
+    for (int i = 0; i < n_mine; i += 2) {
+        if (i + 1 < n_mine) {
+            if (((i + 1) & 63) == 0) fetch_table(i + 1);
+            issue(i + 1, rb, ok_b);
+        }
+        consume(i, ra, ok_a);
+        if (i + 1 < n_mine) {
+            if (i + 2 < n_mine) {
+                if (((i + 2) & 63) == 0) fetch_table(i + 2);
+                issue(i + 2, ra, ok_a);
+            }
+            consume(i + 1, rb, ok_b);
         }
     }
 
@@ -239,7 +288,6 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 
     __shared__ float s_acc[4][NREP][kDimHead];
     __shared__ float s_ml[4][NREP][2];
-    __shared__ int s_last;
     if (rg == 0) {
 #pragma unroll
         for (int r = 0; r < NREP; ++r) {
@@ -271,6 +319,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         if (nsplit == 1) {
             store_elem<E>(out, (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + d, O / L);
         } else {
+            // Partial state of this split; paged_decode_merge_kernel combines them.
             const int64_t slot = ((int64_t)b * H + h) * S + s;
             a.part_acc[slot * kDimHead + d] = O;
             if (d == 0) {
@@ -279,41 +328,41 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
             }
         }
     }
-    if (nsplit == 1) return;
+}
 
-    // Split-KV merge: the last workgroup of this (sequence, head group) to
-    // arrive combines every split's partial state.
-    __threadfence();
-    __syncthreads();
-    int* counter = a.counters + (int64_t)b * gridDim.y + kvhg;
-    if (tid == 0) {
-        const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == nsplit - 1);
+// Combine the split partials of sequences that were split; one workgroup per
+// (sequence, query head), one thread per head dim.  Runs after the split
+// kernel on the same stream, so no cross-workgroup synchronisation is needed.
+template <typename E>
+__global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
+    const int h = blockIdx.x;
+    const int b = blockIdx.y;
+    const int d = threadIdx.x;
+    const int kv_len = a.kv_lens[b];
+    const int npages = kv_len > 0 ? (kv_len + kPage - 1) / kPage : 0;
+    int nsplit = (npages + a.split_pages - 1) / a.split_pages;
+    nsplit = nsplit < a.max_splits ? nsplit : a.max_splits;
+    if (nsplit <= 1) return;
+    const int64_t slot0 = ((int64_t)b * a.n_heads + h) * a.max_splits;
+    float M = kEmptyMax;
+    for (int i = 0; i < nsplit; ++i) M = fmaxf(M, a.part_ml[(slot0 + i) * 2]);
+    float L = 0.0f, O = 0.0f;
+    for (int i = 0; i < nsplit; ++i) {
+        const float f = fast_exp2(a.part_ml[(slot0 + i) * 2] - M);
+        L = fmaf(a.part_ml[(slot0 + i) * 2 + 1], f, L);
+        O = fmaf(a.part_acc[(slot0 + i) * kDimHead + d], f, O);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (int idx = tid; idx < NREP * kDimHead; idx += 256) {
-        const int r = idx / kDimHead, d = idx - r * kDimHead;
-        const int h = h0 + r;
-        const int64_t slot0 = ((int64_t)b * H + h) * S;
-        float M = kEmptyMax;
-        for (int i = 0; i < nsplit; ++i) M = fmaxf(M, a.part_ml[(slot0 + i) * 2]);
-        float L = 0.0f, O = 0.0f;
-        for (int i = 0; i < nsplit; ++i) {
-            const float f = fast_exp2(a.part_ml[(slot0 + i) * 2] - M);
-            L = fmaf(a.part_ml[(slot0 + i) * 2 + 1], f, L);
-            O = fmaf(a.part_acc[(slot0 + i) * kDimHead + d], f, O);
-        }
-        store_elem<E>(out, (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + d, O / L);
-    }
-    if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    store_elem<E>(reinterpret_cast<char*>(a.out), (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + d,
+                  O / L);
 }
 
 template <typename E, int NREP>
 static hipError_t launch_t(const DecodeArgs& a, int grid_splits, int grid_heads, int num_seqs, hipStream_t st) {
     dim3 grid(grid_splits, grid_heads, num_seqs);
     hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), grid, dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || grid_splits <= 1) return e;
+    hipLaunchKernelGGL((paged_decode_merge_kernel<E>), dim3(a.n_heads, num_seqs), dim3(kDimHead), 0, st, a);
     return hipGetLastError();
 }
 

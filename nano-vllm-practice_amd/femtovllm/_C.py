@@ -95,8 +95,8 @@ def _dtype_code(t: torch.Tensor, fn: str) -> int:
     return code
 
 
-# Split-KV workspaces, one per (device, stream): zero-filled once, the
-# kernel leaves its counters at zero after every call.
+# Split-KV workspaces, one per (device, stream), grown on demand; calls on
+# one stream are ordered, so they can share it.
 _workspaces: dict = {}
 
 
@@ -107,7 +107,7 @@ def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_
     key = (device.index, _stream(device))
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(nbytes + 256, dtype=torch.uint8, device=device)
+        ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     ptr = ws.data_ptr()
     aligned = (ptr + 255) & ~255

@@ -81,8 +81,9 @@ def test_gemv_validation_errors(C):
     assert _gemv(C, dtype=7) == 2
     assert _gemv(C, q=8) == 1 and "aligned" in last()
     assert _gemv(C, ps2=100) == 1 and "strides" in last()
+    assert _gemv(C, nb=0) == 1 and "at least one block" in last()
     assert _gemv(C, nseq=0) == 0  # nothing to do
-    # a multi-split plan without a workspace is rejected before launch
+    # a split plan without a workspace is rejected before launch
     assert _gemv(C, maxkv=8192, nseq=64) == 1 and "workspace" in last()
 
 

@@ -112,12 +112,41 @@ def test_decode_strided_q_matches_contiguous(ops, gpu):
 
 
 def test_decode_back_to_back_calls_reuse_workspace(ops, gpu):
-    """The split-merge counters are left at zero: consecutive calls stay correct."""
+    """Consecutive calls of different sizes share the per-stream workspace."""
     big = workloads.make_paged_workload("ws1", [(5000, 1)] * 3 + [(200, 1)], 16, 8, seed=15)
     small = workloads.make_paged_workload("ws2", [(3000, 1), (100, 1)], 16, 8, seed=16)
     for w in (big, small, big):
         out, q, meta = run_decode(ops, w, gpu)
         assert_close(out, oracle_decode(w, q, meta), torch.bfloat16, f"workspace reuse {w.name}")
+
+
+def test_decode_shape_changes_share_workspace(ops, gpu):
+    """Regression: calls of different shapes share one workspace.
+
+    An earlier design kept split counters in the workspace at a shape-
+    dependent offset, so a later call could find an earlier call's partials
+    there; any state carried between calls in the workspace would fail here.
+    """
+    shapes = [
+        ("a", [(L - 1, 1) for L in (4000, 3000, 2500, 100) * 16], 16, 8),
+        ("b", [(L - 1, 1) for L in (230, 273, 161, 269, 98, 16, 17)], 16, 8),
+        ("c", [(L - 1, 1) for L in (900, 1800)], 32, 8),
+        ("d", [(L - 1, 1) for L in (700, 60, 1300)], 8, 8),
+    ]
+    for name, chunks, H, KVH in shapes:
+        w = workloads.make_paged_workload(name, chunks, H, KVH, dtype=torch.float16, seed=len(chunks) + H)
+        out, q, meta = run_decode(ops, w, gpu)
+        assert_close(out, oracle_decode(w, q, meta), torch.bfloat16, f"shape change {name}")
+
+
+def test_decode_large_batch_small_splits(ops, gpu, monkeypatch):
+    """1100 sequences split every 8 pages: a large split grid and merge grid."""
+    monkeypatch.setenv("FEMTO_DECODE_SPLIT_PAGES", "8")
+    rng = np.random.default_rng(19)
+    lens = [int(x) for x in rng.integers(1, 300, size=1100)]
+    w = workloads.make_paged_workload("many", [(L - 1, 1) for L in lens], 16, 8, seed=19)
+    out, q, meta = run_decode(ops, w, gpu)
+    assert_close(out, oracle_decode(w, q, meta), torch.bfloat16, "1100 sequences")
 
 
 def test_decode_out_of_pool_block_is_a_zero_page(ops, gpu):

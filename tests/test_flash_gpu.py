@@ -72,7 +72,8 @@ def test_dense_equals_paged_identity_table(C, ops, gpu):
 def test_dense_errors(C, gpu):
     q = rand((1, 2, 8, 128), torch.bfloat16, 7).to(gpu)
     with pytest.raises(RuntimeError):
-        C.FlashAttentionWarpCuda(q, q[:, :1, :5], q[:, :1, :5])  # k / v not contiguous
+        kt = q.transpose(2, 3).contiguous().transpose(2, 3)  # same shape, not contiguous
+        C.FlashAttentionWarpCuda(q, kt, kt)
     with pytest.raises(RuntimeError):
         C.FlashAttentionWarpCuda(q.float(), q.float(), q.float())
     with pytest.raises(RuntimeError):
