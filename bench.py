@@ -11,11 +11,15 @@ blocks.  One step = one ``femtovllm.ops.paged_attention_gemv`` call over the
 batch.  ``value`` = algorithmic HBM bytes (K and V once per KV head, Q, O,
 block-table entries, kv_lens) / mean kernel time, in GB/s.
 
-Timing: every step is [L2/MALL flush by a 1 GiB write][spin][start event]
-[op][end event] on torch's current stream, the stream the op launches its
-kernel on; ``ms_per_step`` is the mean start->end time over K steps after W
-warm-up steps, bracketed by torch.cuda.synchronize().  Inputs are resident
-in HBM before timing starts.
+Timing: every step is [cache flush][spin][start event][op][end event] on
+torch's current stream, the stream the op launches its kernels on;
+``ms_per_step`` is the mean start->end time over K steps after W warm-up
+steps, bracketed by torch.cuda.synchronize().  Inputs are resident in HBM
+before timing starts.  The flush *reads* a 1 GiB buffer, which evicts the
+pool from L2 and the 256 MB MALL and leaves the caches clean; a flush that
+writes 1 GiB instead leaves ~256 MB of dirty lines whose write-back then
+competes with the measured kernel (that figure is reported alongside as
+``ms_per_step_write_flush``).
 
 Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
 long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
@@ -61,9 +65,10 @@ class Timer:
 
     def __init__(self, torch, device):
         self.torch = torch
-        self.flush = torch.empty(1 << 30, dtype=torch.uint8, device=device)
+        self.rbuf = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        self.wbuf = torch.empty(1 << 30, dtype=torch.uint8, device=device)
 
-    def run(self, fn, steps, warmup):
+    def run(self, fn, steps, warmup, write_flush=False):
         torch = self.torch
         for _ in range(warmup):
             fn()
@@ -71,7 +76,10 @@ class Timer:
         evs = []
         t0 = time.perf_counter()
         for _ in range(steps):
-            self.flush.zero_()
+            if write_flush:
+                self.wbuf.zero_()
+            else:
+                self.rbuf.sum()
             torch.cuda._sleep(200_000)
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
@@ -160,6 +168,7 @@ def main():
         torch.cuda.synchronize()
         assert not torch.isnan(out.float()).any(), "decode produced NaN"
         mean_ms, med_ms, wall = timer.run(fn, K, W)
+        wf_ms, _, _ = timer.run(fn, K, 1, write_flush=True)
         nbytes = workloads.decode_bytes(w)
         gbs = nbytes / (mean_ms * 1e-3) / 1e9
         result = {
@@ -194,9 +203,10 @@ def main():
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
                 "traffic": pmc_traffic("paged_decode_bf16_qwen3_0.6b_b64"),
                 "algorithmic_bytes_per_launch": nbytes,
-                "kernel": "paged_decode_kernel<BF16,2>",
+                "kernel": "paged_decode_kernel<BF16,2> + paged_decode_merge_kernel<BF16> (both inside the timed region)",
             },
             "median_ms_per_step": round(med_ms, 5),
+            "ms_per_step_write_flush": round(wf_ms, 5),
             "wall_s_timed_region": round(wall, 3),
         }
         del wd

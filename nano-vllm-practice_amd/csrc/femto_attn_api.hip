@@ -6,6 +6,7 @@
 // csrc/flash_attention/flash_attention_warp.cu:306-349) for what can be seen
 // from raw pointers and sizes; tensor-level checks (device, rank, int32
 // index dtype) live in the Python layer that owns the tensors.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <string>
@@ -54,31 +55,25 @@ int env_int(const char* name, int fallback) {
 
 namespace femto {
 
-DecodePlan plan_paged_decode(int num_seqs, int n_heads, int n_kv_heads, int max_kv_len) {
+DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len) {
     DecodePlan p;
     const int n_rep = (n_kv_heads > 0) ? n_heads / n_kv_heads : 1;
     p.nrep_tile = (n_rep % 8 == 0) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
     const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
-    // Pages per workgroup: the smallest power of two (8..256) that keeps
-    // the estimated number of workgroups (average context = max / 2, two
-    // query heads per KV head) at or below 4096, i.e. a few per CU in
-    // flight with a small split-merge overhead.
-    int sp = env_int("FEMTO_DECODE_SPLIT_PAGES", 0);
-    if (sp == 0) {
-        const double est = (double)num_seqs * (max_pages / 2.0) * (n_heads / 2.0 > 1.0 ? n_heads / 2.0 : 1.0);
-        sp = 8;
-        while (sp < 256 && est / sp > 4096.0) sp *= 2;
-    }
-    p.split_pages = sp;
-    p.max_splits = (max_pages + sp - 1) / sp;
-    if (p.max_splits < 1) p.max_splits = 1;
+    // A wave's slice is at least min_chunk_pages long, so a sequence is cut
+    // into at most max_slots - 1 slices (+1 for a slice straddling its start).
+    p.min_chunk_pages = env_int("FEMTO_DECODE_MIN_CHUNK_PAGES", 0);
+    if (p.min_chunk_pages == 0) p.min_chunk_pages = std::max(4, (max_pages + 31) / 32);
+    p.min_chunk_pages = std::max(p.min_chunk_pages, (max_pages + 126) / 127);  // merge kernel: <= 128 slots
+    p.max_slots = (max_pages + p.min_chunk_pages - 1) / p.min_chunk_pages + 1;
     return p;
 }
 
-size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_splits) {
-    if (max_splits <= 1 || num_seqs <= 0) return 0;
-    const size_t slots = (size_t)num_seqs * n_heads * max_splits;
-    return slots * (kDimHead + 2) * sizeof(float);
+size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots) {
+    if (num_seqs <= 0) return 0;
+    const size_t slots = (size_t)num_seqs * n_heads * max_slots;
+    size_t bytes = slots * (kDimHead + 2) * sizeof(float);
+    return bytes + (size_t)num_seqs * sizeof(int);
 }
 
 }  // namespace femto
@@ -93,8 +88,8 @@ int femto_attn_dim_head(void) { return femto::kDimHead; }
 
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
     if (num_seqs <= 0 || n_heads <= 0) return 0;
-    const femto::DecodePlan p = femto::plan_paged_decode(num_seqs, n_heads, 1, max_kv_len);
-    return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_splits);
+    const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len);
+    return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_slots);
 }
 
 static int check_paged_common(const char* fn, int dtype, const void* q, const void* out, const void* k_pool,
@@ -144,9 +139,9 @@ int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, 
                                 q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride);
     if (rc != FEMTO_OK) return rc;
 
-    const femto::DecodePlan plan = femto::plan_paged_decode(num_seqs, n_heads, n_kv_heads, max_kv_len);
-    const size_t need = femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_splits);
-    if (need > 0 && (!workspace || workspace_bytes < need || !aligned(workspace, 256)))
+    const femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len);
+    const size_t need = femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_slots);
+    if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: workspace of " + std::to_string(need) +
                                            " bytes (256-byte aligned) required, got " +
                                            std::to_string(workspace_bytes));
@@ -171,16 +166,16 @@ int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, 
     a.n_heads = n_heads;
     a.n_rep = n_heads / n_kv_heads;
     a.head_groups = a.n_rep / plan.nrep_tile;
-    a.split_pages = plan.split_pages;
-    a.max_splits = plan.max_splits;
+    a.num_seqs = num_seqs;
+    a.grid_heads = n_heads / plan.nrep_tile;
+    a.min_chunk_pages = plan.min_chunk_pages;
+    a.max_slots = plan.max_slots;
     a.scale_log2 = scale_log2(head_dim);
-    if (need > 0) {
-        const size_t slots = (size_t)num_seqs * n_heads * plan.max_splits;
-        a.part_acc = static_cast<float*>(workspace);
-        a.part_ml = a.part_acc + slots * femto::kDimHead;
-    }
-    return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, plan.max_splits, num_seqs,
-                                                 static_cast<hipStream_t>(stream)),
+    const size_t slots = (size_t)num_seqs * n_heads * plan.max_slots;
+    a.part_acc = static_cast<float*>(workspace);
+    a.part_ml = a.part_acc + slots * femto::kDimHead;
+    a.seq_slots = reinterpret_cast<int*>(a.part_ml + slots * 2);
+    return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, static_cast<hipStream_t>(stream)),
                       "paged_attention_gemv launch");
 }
 

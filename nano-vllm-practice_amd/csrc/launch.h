@@ -21,24 +21,28 @@ struct DecodeArgs {
     int64_t table_stride;
     int num_pages_per_seq;
     const int32_t* kv_lens;
+    int num_seqs;
     int n_heads, n_rep, head_groups;
-    int split_pages, max_splits;
+    int grid_heads;       // n_heads / nrep_tile: KV head groups
+    int waves_per_group;  // set by the launcher from the resident wave count
+    int min_chunk_pages;  // lower bound on a wave's slice length
+    int max_slots;        // partial slots per (sequence, head)
     float scale_log2;
-    float* part_acc;  // [num_seqs][n_heads][max_splits][128]
-    float* part_ml;   // [num_seqs][n_heads][max_splits][2]
+    float* part_acc;  // [num_seqs][n_heads][max_slots][128]
+    float* part_ml;   // [num_seqs][n_heads][max_slots][2]
+    int* seq_slots;   // [num_seqs] partial slots written for the sequence
 };
 
-// Split size (pages per workgroup) and split count used for a decode call.
+// Work split of a decode call.
 struct DecodePlan {
-    int nrep_tile;   // query heads per workgroup
-    int split_pages;
-    int max_splits;  // grid.x
+    int nrep_tile;        // query heads per wave
+    int min_chunk_pages;  // pages
+    int max_slots;
 };
-DecodePlan plan_paged_decode(int num_seqs, int n_heads, int n_kv_heads, int max_kv_len);
-size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_splits);
+DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len);
+size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots);
 
-hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int grid_splits, int num_seqs,
-                               hipStream_t st);
+hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st);
 
 struct PrefillArgs {
     const void* q;

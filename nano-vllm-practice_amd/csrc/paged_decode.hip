@@ -101,291 +101,371 @@ struct PageRegs {
     RowSlice<E> k[4], v[4];
 };
 
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, kWave);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+__device__ __forceinline__ int pages_of(int kv_len) { return kv_len > 0 ? (kv_len + kPage - 1) / kPage : 0; }
+
+// Load-balanced split-KV decode.  Every wave is an independent worker: the
+// pages of all sequences are concatenated (per KV head group) and cut into
+// equal slices of C pages, one slice per wave, with as many waves as the GPU
+// holds at once.  A wave walks its slice sequence by sequence and leaves one
+// partial softmax state per (sequence segment, query head); the merge kernel
+// combines them.  Slice s of sequence b is partial slot s - first_wave(b).
 template <typename E, int NREP>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     constexpr int EB = E::kBytes;
-    const int s = blockIdx.x;
-    const int kvhg = blockIdx.y;
-    const int b = blockIdx.z;
-    const int kvh = kvhg / a.head_groups;
-    const int hg = kvhg - kvh * a.head_groups;
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int grp = gw / a.waves_per_group;
+    const int wi = gw - grp * a.waves_per_group;
+    if (grp >= a.grid_heads) return;  // waves are independent: no barriers below
+    const int kvh = grp / a.head_groups;
+    const int hg = grp - kvh * a.head_groups;
     const int h0 = kvh * a.n_rep + hg * NREP;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
     const int rg = lane >> 4;
     const int c = lane & 15;
+    const int B = a.num_seqs;
 
-    const int kv_len = a.kv_lens[b];
-    const int npages = kv_len > 0 ? (kv_len + kPage - 1) / kPage : 0;
-    int nsplit = (npages + a.split_pages - 1) / a.split_pages;
-    nsplit = nsplit < (int)gridDim.x ? nsplit : (int)gridDim.x;
-
-    char* out = reinterpret_cast<char*>(a.out);
-    if (kv_len <= 0) {
-        // Empty context: the reference's P.V loop never runs and its zero
-        // accumulator is stored (paged_attention_gemv.cu:203-218).
-        if (s == 0) {
-            for (int idx = tid; idx < NREP * kDimHead; idx += 256) {
-                const int r = idx / kDimHead, d = idx - r * kDimHead;
-                store_elem<E>(out, (int64_t)(h0 + r) * a.out_stride_head + (int64_t)b * a.out_stride_seq + d, 0.0f);
-            }
-        }
-        return;
+    // Pass 1: total pages P and the longest sequence; slice length C.
+    int total = 0, longest = 0;
+#pragma unroll 4
+    for (int i = lane; i < B; i += kWave) {
+        const int pg = pages_of(a.kv_lens[i]);
+        total += pg;
+        longest = max(longest, pg);
     }
-    if (s >= nsplit) return;
-    const int p0 = s * a.split_pages;
-    const int p1 = (s == nsplit - 1) ? npages : p0 + a.split_pages;
+    total = wave_sum(total);
+    longest = wave_max(longest);
+    int C = (total + a.waves_per_group - 1) / a.waves_per_group;
+    C = max(C, a.min_chunk_pages);
+    C = max(C, (longest + a.max_slots - 2) / (a.max_slots - 1));  // at most max_slots slots per sequence
+    C = max(C, 1);
+    const int x0 = wi * C;
+    if (x0 >= total) return;
+    const int x1 = min(total, x0 + C);
+
+    // Pass 2: the sequence holding page x0.  Lane i of the current 64-wide
+    // chunk keeps kv_len and the exclusive page prefix of sequence base + i.
+    int base = 0, carry = 0, my_len = 0, my_excl = 0, chunk_total = 0;
+    for (;; base += kWave) {
+        const int i = base + lane;
+        my_len = i < B ? a.kv_lens[i] : 0;
+        const int pg = pages_of(my_len);
+        const int incl = wave_incl_scan(pg, lane);
+        my_excl = carry + incl - pg;
+        chunk_total = __shfl(incl, kWave - 1, kWave);
+        if (x0 < carry + chunk_total) break;
+        carry += chunk_total;
+    }
+    // first sequence of the chunk whose pages end after x0 (skips empty ones)
+    const uint64_t after = __ballot(base + lane < B && my_excl + pages_of(my_len) > x0);
+    int b = base + __builtin_ctzll(after);
 
     // Query rows of the NREP heads, in this lane's 8 dims.
     float qf[NREP][8];
     const char* qbase = reinterpret_cast<const char*>(a.q);
-#pragma unroll
-    for (int r = 0; r < NREP; ++r) {
-        RowSlice<E> qs;
-        qs.load(qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)b * a.q_stride_seq) * EB, c);
-        qs.to_float(qf[r]);
-    }
-
-    float m[NREP], l[NREP], acc[NREP][8];
-#pragma unroll
-    for (int r = 0; r < NREP; ++r) {
-        m[r] = kEmptyMax;
-        l[r] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
-    }
-
-    // This wave owns pages p0 + wave + 4*i, i < n_mine.  Their block ids are
-    // fetched 64 at a time, one per lane, and broadcast with readlane.
-    const int n_mine = (p1 - p0 - wave + 3) >> 2;
-    const int32_t* table = a.tables + (int64_t)b * a.table_stride;
     const char* kpool = reinterpret_cast<const char*>(a.k_pool);
     const char* vpool = reinterpret_cast<const char*>(a.v_pool);
     const int64_t head_off = (int64_t)kvh * a.pool_stride_head;
-    int tbl = -1;
+    const int H = a.n_heads;
 
-    auto fetch_table = [&](int i0) {
-        const int pg = p0 + wave + 4 * (i0 + lane);
-        tbl = (i0 + lane < n_mine && pg < a.num_pages_per_seq) ? table[pg] : -1;
-    };
-    // Issue the 8 (f32: 16) 16-byte loads of page i.  Rows past kv_len are
-    // clamped to the last visible row and blocks outside the pool to block 0,
-    // so every load is in bounds and unconditional; those values are never
-    // used (masked scores, zeroed registers).
-    auto issue = [&](int i, PageRegs<E>& pr, bool& blk_ok) {
-        const int blk = __builtin_amdgcn_readlane(tbl, i & 63);
-        blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
-        const int pg = p0 + wave + 4 * i;
-        const int last_row = kv_len - 1 - pg * kPage;
-        const int64_t page_off = ((int64_t)(blk_ok ? blk : 0) * a.pool_stride_block + head_off) * EB;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = min(rg + 4 * j, last_row);
-            const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
-            pr.k[j].load(kpool + off, c);
-            pr.v[j].load(vpool + off, c);
+    int x = x0;
+    while (x < x1) {
+        if (b - base >= kWave) {  // next chunk of sequences
+            carry += chunk_total;
+            base += kWave;
+            const int i = base + lane;
+            my_len = i < B ? a.kv_lens[i] : 0;
+            const int pg = pages_of(my_len);
+            const int incl = wave_incl_scan(pg, lane);
+            my_excl = carry + incl - pg;
+            chunk_total = __shfl(incl, kWave - 1, kWave);
         }
-    };
-    auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
-        if (!blk_ok) {
-            // A block id outside the pool reads as a page of zeros.
+        const int kv_len = __shfl(my_len, b - base, kWave);
+        const int S = __shfl(my_excl, b - base, kWave);
+        const int npg = pages_of(kv_len);
+        if (npg == 0 || S + npg <= x) {
+            ++b;
+            continue;
+        }
+        const int lp0 = x - S;                 // first page of the segment
+        const int lp1 = min(x1, S + npg) - S;  // one past its last page
+        const int n = lp1 - lp0;
+
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            RowSlice<E> qs;
+            qs.load(qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)b * a.q_stride_seq) * EB, c);
+            qs.to_float(qf[r]);
+        }
+        float m[NREP], l[NREP], acc[NREP][8];
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            m[r] = kEmptyMax;
+            l[r] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+        }
+
+        const int32_t* table = a.tables + (int64_t)b * a.table_stride;
+        int tbl = -1;
+        auto fetch_table = [&](int i0) {
+            const int pg = lp0 + i0 + lane;
+            tbl = (i0 + lane < n && pg < a.num_pages_per_seq) ? table[pg] : -1;
+        };
+        // The 8 (f32: 16) 16-byte loads of page lp0 + i.  Rows past kv_len
+        // are clamped to the last visible row and blocks outside the pool to
+        // block 0, so every load is in bounds and unconditional; those values
+        // are never used (masked scores, zeroed registers).
+        auto issue = [&](int i, PageRegs<E>& pr, bool& blk_ok) {
+            const int blk = __builtin_amdgcn_readlane(tbl, i & 63);
+            blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+            const int pg = lp0 + i;
+            const int last_row = kv_len - 1 - pg * kPage;
+            const int64_t page_off = ((int64_t)(blk_ok ? blk : 0) * a.pool_stride_block + head_off) * EB;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                pr.k[j].zero();
-                pr.v[j].zero();
+                const int row = min(rg + 4 * j, last_row);
+                const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
+                pr.k[j].load(kpool + off, c);
+                pr.v[j].load(vpool + off, c);
             }
-        }
-        const int pg = p0 + wave + 4 * i;
-        float sc[NREP][4];
+        };
+        auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
+            if (!blk_ok) {
+                // A block id outside the pool reads as a page of zeros.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float kf[8];
-            pr.k[j].to_float(kf);
+                for (int j = 0; j < 4; ++j) {
+                    pr.k[j].zero();
+                    pr.v[j].zero();
+                }
+            }
+            const int pg = lp0 + i;
+            float sc[NREP][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float kf[8];
+                pr.k[j].to_float(kf);
+#pragma unroll
+                for (int r = 0; r < NREP; ++r) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(qf[r][e], kf[e], d);
+                    sc[r][j] = d;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool valid = (pg * kPage + rg + 4 * j) < kv_len;
+#pragma unroll
+                for (int r = 0; r < NREP; ++r) {
+                    const float t = row16_sum(sc[r][j]) * a.scale_log2;
+                    sc[r][j] = valid ? t : -INFINITY;
+                }
+            }
+            float vf[4][8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) pr.v[j].to_float(vf[j]);
 #pragma unroll
             for (int r = 0; r < NREP; ++r) {
-                float d = 0.0f;
+                const float mx = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
+                const float mn = fmaxf(m[r], mx);
+                const float al = fast_exp2(m[r] - mn);
+                float p[4];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) d = fmaf(qf[r][e], kf[e], d);
-                sc[r][j] = d;
+                for (int j = 0; j < 4; ++j) p[j] = fast_exp2(sc[r][j] - mn);
+                l[r] = fmaf(l[r], al, (p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float t = acc[r][e] * al;
+                    t = fmaf(p[0], vf[0][e], t);
+                    t = fmaf(p[1], vf[1][e], t);
+                    t = fmaf(p[2], vf[2][e], t);
+                    t = fmaf(p[3], vf[3][e], t);
+                    acc[r][e] = t;
+                }
+                m[r] = mn;
             }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bool valid = (pg * kPage + rg + 4 * j) < kv_len;
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) {
-                const float t = row16_sum(sc[r][j]) * a.scale_log2;
-                sc[r][j] = valid ? t : -INFINITY;
-            }
-        }
-        float vf[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pr.v[j].to_float(vf[j]);
-#pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-            const float mx = fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3]));
-            const float mn = fmaxf(m[r], mx);
-            const float al = fast_exp2(m[r] - mn);
-            float p[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p[j] = fast_exp2(sc[r][j] - mn);
-            l[r] = fmaf(l[r], al, (p[0] + p[1]) + (p[2] + p[3]));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                float t = acc[r][e] * al;
-                t = fmaf(p[0], vf[0][e], t);
-                t = fmaf(p[1], vf[1][e], t);
-                t = fmaf(p[2], vf[2][e], t);
-                t = fmaf(p[3], vf[3][e], t);
-                acc[r][e] = t;
-            }
-            m[r] = mn;
-        }
-    };
+        };
 
-    // Two pages in flight per wave: page i+1 loads while page i computes.
-    PageRegs<E> ra, rb;
-    bool ok_a = false, ok_b = false;
-    if (n_mine > 0) {
+        // Two pages in flight: page i+1 loads while page i computes.
+        PageRegs<E> ra, rb;
+        bool ok_a = false, ok_b = false;
         fetch_table(0);
         issue(0, ra, ok_a);
-    }
-    for (int i = 0; i < n_mine; i += 2) {
-        if (i + 1 < n_mine) {
-            if (((i + 1) & 63) == 0) fetch_table(i + 1);
-            issue(i + 1, rb, ok_b);
-        }
-        consume(i, ra, ok_a);
-        if (i + 1 < n_mine) {
-            if (i + 2 < n_mine) {
-                if (((i + 2) & 63) == 0) fetch_table(i + 2);
-                issue(i + 2, ra, ok_a);
+        for (int i = 0; i < n; i += 2) {
+            if (i + 1 < n) {
+                if (((i + 1) & 63) == 0) fetch_table(i + 1);
+                issue(i + 1, rb, ok_b);
             }
-            consume(i + 1, rb, ok_b);
-        }
-    }
-
-    // Merge the four DPP rows of the wave (they hold the same dims).
-#pragma unroll
-    for (int r = 0; r < NREP; ++r) {
-#pragma unroll
-        for (int sh = 16; sh <= 32; sh *= 2) {
-            const float mo = shfl_xor_f32(m[r], sh);
-            const float lo = shfl_xor_f32(l[r], sh);
-            const float mn = fmaxf(m[r], mo);
-            const float fa = fast_exp2(m[r] - mn);
-            const float fb = fast_exp2(mo - mn);
-            l[r] = l[r] * fa + lo * fb;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float ao = shfl_xor_f32(acc[r][e], sh);
-                acc[r][e] = acc[r][e] * fa + ao * fb;
+            consume(i, ra, ok_a);
+            if (i + 1 < n) {
+                if (i + 2 < n) {
+                    if (((i + 2) & 63) == 0) fetch_table(i + 2);
+                    issue(i + 2, ra, ok_a);
+                }
+                consume(i + 1, rb, ok_b);
             }
-            m[r] = mn;
         }
-    }
 
-    __shared__ float s_acc[4][NREP][kDimHead];
-    __shared__ float s_ml[4][NREP][2];
-    if (rg == 0) {
+        // Merge the four DPP rows (same dims, different keys).
 #pragma unroll
         for (int r = 0; r < NREP; ++r) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) s_acc[wave][r][RowSlice<E>::dim(c, e)] = acc[r][e];
-            if (c == 0) {
-                s_ml[wave][r][0] = m[r];
-                s_ml[wave][r][1] = l[r];
+            for (int sh = 16; sh <= 32; sh *= 2) {
+                const float mo = shfl_xor_f32(m[r], sh);
+                const float lo = shfl_xor_f32(l[r], sh);
+                const float mn = fmaxf(m[r], mo);
+                const float fa = fast_exp2(m[r] - mn);
+                const float fb = fast_exp2(mo - mn);
+                l[r] = l[r] * fa + lo * fb;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float ao = shfl_xor_f32(acc[r][e], sh);
+                    acc[r][e] = acc[r][e] * fa + ao * fb;
+                }
+                m[r] = mn;
             }
         }
-    }
-    __syncthreads();
 
-    const int H = a.n_heads;
-    const int S = a.max_splits;
-    for (int idx = tid; idx < NREP * kDimHead; idx += 256) {
-        const int r = idx / kDimHead, d = idx - r * kDimHead;
-        float M = s_ml[0][r][0];
+        // Partial state of this segment.
+        const int slot = wi - S / C;
+        if (rg == 0) {
 #pragma unroll
-        for (int w = 1; w < 4; ++w) M = fmaxf(M, s_ml[w][r][0]);
-        float L = 0.0f, O = 0.0f;
+            for (int r = 0; r < NREP; ++r) {
+                const int64_t sl = ((int64_t)b * H + h0 + r) * a.max_slots + slot;
+                float* dst = a.part_acc + sl * kDimHead;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float f = fast_exp2(s_ml[w][r][0] - M);
-            L = fmaf(s_ml[w][r][1], f, L);
-            O = fmaf(s_acc[w][r][d], f, O);
-        }
-        const int h = h0 + r;
-        if (nsplit == 1) {
-            store_elem<E>(out, (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + d, O / L);
-        } else {
-            // Partial state of this split; paged_decode_merge_kernel combines them.
-            const int64_t slot = ((int64_t)b * H + h) * S + s;
-            a.part_acc[slot * kDimHead + d] = O;
-            if (d == 0) {
-                a.part_ml[slot * 2] = M;
-                a.part_ml[slot * 2 + 1] = L;
+                for (int e = 0; e < 8; ++e) dst[RowSlice<E>::dim(c, e)] = acc[r][e];
+                if (c == 0) {
+                    a.part_ml[sl * 2] = m[r];
+                    a.part_ml[sl * 2 + 1] = l[r];
+                }
             }
         }
+        if (lane == 0 && grp == 0 && lp1 == npg) a.seq_slots[b] = slot + 1;  // last segment: slot count
+        x = S + lp1;
+        ++b;
     }
 }
 
-// Combine the split partials of sequences that were split; one workgroup per
-// (sequence, query head), one thread per head dim.  Runs after the split
-// kernel on the same stream, so no cross-workgroup synchronisation is needed.
+// Final softmax merge: one workgroup per (sequence, query head), one thread
+// per head dim.  Runs after the split kernel on the same stream.
 template <typename E>
 __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
+    __shared__ float s_w[128];
+    __shared__ float s_l;
     const int h = blockIdx.x;
     const int b = blockIdx.y;
-    const int d = threadIdx.x;
-    const int kv_len = a.kv_lens[b];
-    const int npages = kv_len > 0 ? (kv_len + kPage - 1) / kPage : 0;
-    int nsplit = (npages + a.split_pages - 1) / a.split_pages;
-    nsplit = nsplit < a.max_splits ? nsplit : a.max_splits;
-    if (nsplit <= 1) return;
-    const int64_t slot0 = ((int64_t)b * a.n_heads + h) * a.max_splits;
-    float M = kEmptyMax;
-    for (int i = 0; i < nsplit; ++i) M = fmaxf(M, a.part_ml[(slot0 + i) * 2]);
-    float L = 0.0f, O = 0.0f;
-    for (int i = 0; i < nsplit; ++i) {
-        const float f = fast_exp2(a.part_ml[(slot0 + i) * 2] - M);
-        L = fmaf(a.part_ml[(slot0 + i) * 2 + 1], f, L);
-        O = fmaf(a.part_acc[(slot0 + i) * kDimHead + d], f, O);
+    const int t = threadIdx.x;
+    char* out = reinterpret_cast<char*>(a.out);
+    const int64_t o = (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + t;
+    if (a.kv_lens[b] <= 0) {
+        // Empty context: the reference's P.V loop never runs and its zero
+        // accumulator is stored (paged_attention_gemv.cu:203-218).
+        store_elem<E>(out, o, 0.0f);
+        return;
     }
-    store_elem<E>(reinterpret_cast<char*>(a.out), (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + d,
-                  O / L);
+    const int count = a.seq_slots[b];
+    const int64_t sl0 = ((int64_t)b * a.n_heads + h) * a.max_slots;
+    // thread i < count holds slot i's (m, l); wave-reduce the max, then every
+    // slot's weight exp2(m_i - M) goes to LDS.
+    const float mi = t < count ? a.part_ml[(sl0 + t) * 2] : kEmptyMax;
+    const float li = t < count ? a.part_ml[(sl0 + t) * 2 + 1] : 0.0f;
+    float M = mi;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
+    __shared__ float s_m[2];
+    if ((t & 63) == 0) s_m[t >> 6] = M;
+    __syncthreads();
+    M = fmaxf(s_m[0], s_m[1]);
+    const float wi = t < count ? fast_exp2(mi - M) : 0.0f;
+    s_w[t] = wi;
+    float lw = li * wi;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lw += shfl_xor_f32(lw, off);
+    __shared__ float s_ls[2];
+    if ((t & 63) == 0) s_ls[t >> 6] = lw;
+    __syncthreads();
+    if (t == 0) s_l = s_ls[0] + s_ls[1];
+    __syncthreads();
+    float O = 0.0f;
+    const float* src = a.part_acc + sl0 * kDimHead + t;
+    int i = 0;
+    for (; i + 4 <= count; i += 4) {
+        const float v0 = src[(int64_t)(i + 0) * kDimHead], v1 = src[(int64_t)(i + 1) * kDimHead];
+        const float v2 = src[(int64_t)(i + 2) * kDimHead], v3 = src[(int64_t)(i + 3) * kDimHead];
+        O = fmaf(v0, s_w[i], O);
+        O = fmaf(v1, s_w[i + 1], O);
+        O = fmaf(v2, s_w[i + 2], O);
+        O = fmaf(v3, s_w[i + 3], O);
+    }
+    for (; i < count; ++i) O = fmaf(src[(int64_t)i * kDimHead], s_w[i], O);
+    store_elem<E>(out, o, O / s_l);
 }
 
 template <typename E, int NREP>
-static hipError_t launch_t(const DecodeArgs& a, int grid_splits, int grid_heads, int num_seqs, hipStream_t st) {
-    dim3 grid(grid_splits, grid_heads, num_seqs);
-    hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), grid, dim3(256), 0, st, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || grid_splits <= 1) return e;
+static hipError_t launch_t(DecodeArgs a, int num_seqs, hipStream_t st) {
+    // One grid of resident waves; waves_per_group of them per KV head group.
+    static int resident_wgs[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int& per_dev = resident_wgs[dev & 63];
+    if (per_dev == 0) {
+        int cus = 0, per_cu = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<E, NREP>, 256, 0);
+        if (e != hipSuccess) return e;
+        per_dev = cus * (per_cu > 0 ? per_cu : 1);
+    }
+    const int total_waves = per_dev * 4;
+    a.waves_per_group = total_waves / a.grid_heads > 0 ? total_waves / a.grid_heads : 1;
+    const int grid = (a.waves_per_group * a.grid_heads + 3) / 4;
+    hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), dim3(grid), dim3(256), 0, st, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((paged_decode_merge_kernel<E>), dim3(a.n_heads, num_seqs), dim3(kDimHead), 0, st, a);
     return hipGetLastError();
 }
 
 template <typename E>
-static hipError_t launch_e(const DecodeArgs& a, int nrep_tile, int grid_splits, int grid_heads, int num_seqs,
-                           hipStream_t st) {
+static hipError_t launch_e(const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st) {
     switch (nrep_tile) {
-        case 1: return launch_t<E, 1>(a, grid_splits, grid_heads, num_seqs, st);
-        case 2: return launch_t<E, 2>(a, grid_splits, grid_heads, num_seqs, st);
-        case 4: return launch_t<E, 4>(a, grid_splits, grid_heads, num_seqs, st);
-        case 8: return launch_t<E, 8>(a, grid_splits, grid_heads, num_seqs, st);
+        case 1: return launch_t<E, 1>(a, num_seqs, st);
+        case 2: return launch_t<E, 2>(a, num_seqs, st);
+        case 4: return launch_t<E, 4>(a, num_seqs, st);
+        case 8: return launch_t<E, 8>(a, num_seqs, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int grid_splits, int num_seqs,
-                               hipStream_t st) {
-    const int grid_heads = a.n_heads / nrep_tile;
-    if (grid_splits <= 0 || num_seqs <= 0 || grid_heads <= 0) return hipSuccess;
+hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st) {
+    if (num_seqs <= 0 || a.grid_heads <= 0) return hipSuccess;
     switch (dtype) {
-        case kDtypeF32: return launch_e<F32>(a, nrep_tile, grid_splits, grid_heads, num_seqs, st);
-        case kDtypeF16: return launch_e<F16>(a, nrep_tile, grid_splits, grid_heads, num_seqs, st);
-        case kDtypeBF16: return launch_e<BF16>(a, nrep_tile, grid_splits, grid_heads, num_seqs, st);
+        case kDtypeF32: return launch_e<F32>(a, nrep_tile, num_seqs, st);
+        case kDtypeF16: return launch_e<F16>(a, nrep_tile, num_seqs, st);
+        case kDtypeBF16: return launch_e<BF16>(a, nrep_tile, num_seqs, st);
         default: return hipErrorInvalidValue;
     }
 }
