@@ -201,6 +201,8 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
     if (rc != FEMTO_OK) return rc;
     if (out_stride_head % 4 || out_stride_token % 4)
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: out strides must be multiples of 8 bytes");
+    if (pool_stride_row < 0 || pool_stride_row > (1 << 24))
+        return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: pool row stride out of range");
 
     femto::PrefillArgs a{};
     a.q = q;
@@ -257,6 +259,8 @@ int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int6
         if (s % 8) return fail(FEMTO_ERR_INVALID, "flash_attention: q/k/v strides must be multiples of 16 bytes");
     if (out_stride_batch % 4 || out_stride_head % 4 || out_stride_token % 4)
         return fail(FEMTO_ERR_INVALID, "flash_attention: out strides must be multiples of 8 bytes");
+    if (k_stride_token < 0 || k_stride_token > (1 << 24) || v_stride_token < 0 || v_stride_token > (1 << 24))
+        return fail(FEMTO_ERR_INVALID, "flash_attention: k/v token stride out of range");
 
     femto::PrefillArgs a{};
     a.q = q;

@@ -13,15 +13,21 @@
 //  * a workgroup (4 waves) owns G query heads that share one KV head and a
 //    block of BT = 32 * 4 / G tokens; each wave owns 32 tokens of one head,
 //    so K/V tiles staged in LDS are used by 4 x 32 query rows;
-//  * KV is consumed in tiles of 64 keys (4 pages).  K is stored row-major
-//    [key][dim]; V is transposed on its way into LDS to [dim][key];
+//  * KV is consumed in tiles of 64 keys (4 pages), double-buffered in LDS.
+//    Both K and V are copied HBM -> LDS with global_load_lds_dwordx4 (no
+//    VGPR staging, no VALU), wave w fetching page w of the tile.  Rows are
+//    kept row-major [key][dim] with 16-byte chunks XOR-swizzled by row, so
+//    the K operand reads (ds_read_b128) and the transposed V operand reads
+//    (ds_read_b64_tr_b16) are bank-conflict free;
 //  * per tile and wave: S^T(64 x 32) = K . Q^T with 16 MFMAs (Q stays in
 //    registers as the B operand), online softmax with the query index equal
 //    to the lane (mod 32), then O^T(128 x 32) += V^T . P^T with 16 MFMAs, P
 //    taken straight from the S^T accumulators, rounded to the storage type
 //    (the reference's Triton kernel rounds P the same way, line 153-155);
 //  * causal tile skipping: a wave skips tiles past its largest visible key
-//    and applies the mask only on tiles that cross its smallest limit;
+//    and applies the mask only on tiles that cross its smallest limit; the
+//    running max moves lazily (only when a row max grows by > 2^8), so O is
+//    rarely rescaled;
 //  * tiles of one sequence are issued heaviest (last) first, and the work
 //    list is laid out so each XCD (workgroup id mod 8) gets a contiguous
 //    range of KV heads, keeping a head's pages in one L2.
@@ -31,9 +37,44 @@
 namespace femto {
 
 constexpr int kKvTile = 64;
-constexpr int kKPitch = kDimHead + 8;  // elements per K row in LDS (272 B)
-constexpr int kVPitch = kKvTile + 4;   // elements per V^T row in LDS (136 B)
+constexpr int kStages = 2;
+constexpr int kRowBytes = kDimHead * 2;                // 256
+constexpr int kTileBytes = kKvTile * kRowBytes;        // 16 KB per K or V tile
 constexpr float kEmptyMaxP = -1.0e30f;
+
+// One page of zeros: the source of every load whose block id lies outside
+// the pool, so such a page reads as zeros without a branch.
+__device__ __attribute__((aligned(16))) uint16_t g_zero_page[kPage * kDimHead];
+
+// 16-byte chunk c of LDS row r lives at chunk position c ^ swz(r).
+__device__ __forceinline__ int swz_k(int r) { return r & 15; }
+__device__ __forceinline__ int swz_v(int r) { return (r & 7) << 1; }
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// 16 bytes per lane from global memory (uniform base + per-lane offset)
+// straight into LDS at lds_base + 16 * lane.  Issued through asm so the
+// compiler does not order later LDS reads of the other stage behind it; the
+// kernel waits for these copies itself (vmcnt) before the stage is read.
+// base and lds_base must be the same in every lane of the wave.
+__device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds_base) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | lo;
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(sb), "s"(m0v)
+        : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
 
 __device__ __forceinline__ int block_incl_scan(int v, int* s_wsum, int& total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -57,11 +98,11 @@ __device__ __forceinline__ int block_incl_scan(int v, int* s_wsum, int& total) {
 }
 
 template <typename E, int G, bool PAGED>
-__global__ __launch_bounds__(256) void attention_mfma_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_mfma_kernel(PrefillArgs a) {
     constexpr int EB = 2;
     constexpr int BT = 32 * (4 / G);
-    __shared__ __attribute__((aligned(16))) uint16_t Ks[kKvTile * kKPitch];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[kDimHead * kVPitch];
+    // [stage][0 = K, 1 = V][64 keys x 256 B]
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages][2][kTileBytes];
     __shared__ int s_wsum[4];
     __shared__ int s_seq, s_ltile;
     __shared__ int s_kend[4];
@@ -155,55 +196,81 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(PrefillArgs a) {
         for (int kk = 0; kk < 8; ++kk) qreg[kk] = qvalid ? ld16(qrow + (16 * kk + 8 * h2) * EB) : u32x4{0, 0, 0, 0};
     }
 
-    // ---- KV tile staging ------------------------------------------------
+    // ---- KV staging: wave w copies page w of each tile (16 keys x 256 B of
+    // K and of V) with 4 + 4 direct-to-LDS loads; in load j, lane i writes
+    // LDS row 16w + 4j + i/16, chunk position i%16, and so fetches logical
+    // chunk (i%16) ^ swz(row).
     const char* kbase_p = reinterpret_cast<const char*>(a.k);
     const char* vbase_p = reinterpret_cast<const char*>(a.v);
     const int32_t* table = PAGED ? a.tables + (int64_t)b * a.table_stride : nullptr;
-    const int c16 = tid & 15;
-    const int r16 = tid >> 4;
-
-    auto key_row = [&](const char* base, int key, int64_t s0, int64_t s1, int64_t s2, bool& ok) -> const char* {
-        ok = key < kv_len;
-        if constexpr (PAGED) {
-            const int page = key >> 4;
-            const int blk = (ok && page < a.num_pages_per_seq) ? table[page] : -1;
-            ok = ok && blk >= 0 && (int64_t)blk < a.num_blocks;
-            return base + ((int64_t)blk * s0 + (int64_t)kvh * s1 + (int64_t)(key & 15) * s2) * EB;
-        } else {
-            return base + ((int64_t)b * s0 + (int64_t)kvh * s1 + (int64_t)key * s2) * EB;
-        }
+    const int npages_tbl = PAGED ? min(a.num_pages_per_seq, (kv_len + kPage - 1) / kPage) : 0;
+    const int lrow = lane >> 4;  // row within the load's group of 4
+    const int lpos = lane & 15;
+    int koff[4], voff[4];        // byte offset of this lane's chunk inside its row
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + lrow;
+        koff[j] = ((lpos ^ swz_k(r)) << 4);
+        voff[j] = ((lpos ^ swz_v(r)) << 4);
+    }
+    // Block ids for this wave's page of tiles tbase .. tbase+63, one per lane.
+    int tbl = -1, tbase = 0;
+    auto fetch_table = [&](int it0) {
+        tbase = it0;
+        const int pg = 4 * (it0 + lane) + wave;
+        tbl = (PAGED && pg < npages_tbl) ? table[pg] : -1;
     };
 
-    u32x4 kreg[4], vreg[4];
-    auto load_tile = [&](int kb) {
+    auto issue_tile = [&](int it, int stage) {
+        const int key0 = it * kKvTile + 16 * wave;  // first key of this wave's page
+        // Keys past kv_len read the last visible key's row (finite data,
+        // masked later); pages wholly past kv_len read that key's page.
+        const int kc = key0 < kv_len ? key0 : kv_len - 1;
+        const int last_row = kv_len - 1 - (kc & ~15);
+        const char* kp;
+        const char* vp;
+        int rs_k, rs_v;
+        if constexpr (PAGED) {
+            int blk = -1;
+            if (key0 < kv_len) {
+                blk = __builtin_amdgcn_readlane(tbl, it - tbase);
+            } else {
+                const int pg = kc >> 4;
+                blk = pg < npages_tbl ? table[pg] : -1;
+                blk = __builtin_amdgcn_readfirstlane(blk);
+            }
+            const bool ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+            kp = ok ? kbase_p + ((int64_t)blk * a.k_stride0 + (int64_t)kvh * a.k_stride1) * EB
+                    : reinterpret_cast<const char*>(g_zero_page);
+            vp = ok ? vbase_p + ((int64_t)blk * a.v_stride0 + (int64_t)kvh * a.v_stride1) * EB
+                    : reinterpret_cast<const char*>(g_zero_page);
+            rs_k = ok ? (int)a.k_stride2 * EB : kRowBytes;
+            rs_v = ok ? (int)a.v_stride2 * EB : kRowBytes;
+        } else {
+            const int k16 = kc & ~15;
+            kp = kbase_p + ((int64_t)b * a.k_stride0 + (int64_t)kvh * a.k_stride1 + (int64_t)k16 * a.k_stride2) * EB;
+            vp = vbase_p + ((int64_t)b * a.v_stride0 + (int64_t)kvh * a.v_stride1 + (int64_t)k16 * a.v_stride2) * EB;
+            rs_k = (int)a.k_stride2 * EB;
+            rs_v = (int)a.v_stride2 * EB;
+        }
+        const uint32_t kd = lds_addr(&smem[stage][0][(16 * wave) * kRowBytes]);
+        const uint32_t vd = lds_addr(&smem[stage][1][(16 * wave) * kRowBytes]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            bool ok;
-            const char* p = key_row(kbase_p, kb + 16 * j + r16, a.k_stride0, a.k_stride1, a.k_stride2, ok);
-            kreg[j] = ok ? ld16(p + 16 * c16) : u32x4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            bool ok;
-            const char* p = key_row(vbase_p, kb + 4 * r16 + i, a.v_stride0, a.v_stride1, a.v_stride2, ok);
-            vreg[i] = ok ? ld16(p + 16 * c16) : u32x4{0, 0, 0, 0};
+            const int row = min(4 * j + lrow, last_row);
+            lds_dma16(kp, (uint32_t)(row * rs_k + koff[j]), kd + j * 1024);
+            lds_dma16(vp, (uint32_t)(row * rs_v + voff[j]), vd + j * 1024);
         }
     };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) st16(&Ks[(16 * j + r16) * kKPitch + 8 * c16], kreg[j]);
-        // V rows 4*r16 .. 4*r16+3, dims 8*c16 .. +7  ->  V^T[dim][4 keys]
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int word = e >> 1;
-            const int sh = (e & 1) * 16;
-            const uint32_t v0 = (vreg[0][word] >> sh) & 0xffffu;
-            const uint32_t v1 = (vreg[1][word] >> sh) & 0xffffu;
-            const uint32_t v2 = (vreg[2][word] >> sh) & 0xffffu;
-            const uint32_t v3 = (vreg[3][word] >> sh) & 0xffffu;
-            *reinterpret_cast<u32x2*>(&Vt[(8 * c16 + e) * kVPitch + 4 * r16]) = u32x2{v0 | (v1 << 16), v2 | (v3 << 16)};
-        }
-    };
+
+    // Per-lane constant parts of the LDS operand addresses.
+    const int k_rd = l32 * kRowBytes;  // K row l32 (+ 32 * kb2 rows)
+    const int k_sw = swz_k(l32);
+    // V^T operand via ds_read_b64_tr_b16: in each 16-lane group, lane i
+    // supplies keys (.. + i/4) x dims (.. + 4*(i%4)); lane j then holds dim j.
+    const int gi = lane & 15;
+    const int v_key = 4 * h2 + (gi >> 2);                 // + 16*ks + 8*half
+    const int v_dim = 16 * ((lane >> 4) & 1) + 4 * (gi & 3);  // + 32*dt
 
     f32x16 oacc[4];
 #pragma unroll
@@ -213,75 +280,96 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(PrefillArgs a) {
     const float scale = a.scale_log2;
 
     const int ntiles = (kend + kKvTile - 1) / kKvTile;
-    if (ntiles > 0) load_tile(0);
+    if (ntiles > 0) {
+        fetch_table(0);
+        issue_tile(0, 0);
+    }
     for (int it = 0; it < ntiles; ++it) {
         const int kb = it * kKvTile;
-        __syncthreads();
-        store_tile();
-        __syncthreads();
-        if (it + 1 < ntiles) load_tile(kb + kKvTile);
+        const int stage = it & 1;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile it are in LDS
+        __syncthreads();                     // ... and every wave's; stage ^ 1 is free again
+        if (it + 1 < ntiles) {
+            if (((it + 1 - tbase) & ~63) != 0) fetch_table(it + 1);
+            issue_tile(it + 1, stage ^ 1);  // in flight during this tile's math
+        }
         if (kb >= kend_w) continue;
         const bool need_mask = kb + kKvTile > kfull_w;
+        const uint8_t* ks = smem[stage][0];
+        const uint8_t* vs = smem[stage][1];
 
-        // S^T blocks: keys kb + 32*kb2 + (0..31), queries = lanes.
+        // S^T blocks: keys kb + 32*kb2 + (0..31), queries = lanes (raw scores).
         f32x16 sacc[2];
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
             sacc[kb2] = f32x16{};
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) {
-                const u32x4 ka = *reinterpret_cast<const u32x4*>(&Ks[(32 * kb2 + l32) * kKPitch + 16 * kk + 8 * h2]);
+                const int chunk = (2 * kk + h2) ^ k_sw;
+                const u32x4 ka = *reinterpret_cast<const u32x4*>(ks + k_rd + kb2 * 32 * kRowBytes + (chunk << 4));
                 sacc[kb2] = mfma32x32x16(E{}, ka, qreg[kk], sacc[kb2]);
             }
         }
         // Accumulator i of block kb2 holds key kb + 32*kb2 + 8*(i/4) + 4*h2 + i%4.
-        float mx = kEmptyMaxP;
+        float mx = -INFINITY;
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float s = sacc[kb2][i] * scale;
+                float s = sacc[kb2][i];
                 if (need_mask) {
                     const int key = kb + 32 * kb2 + 8 * (i >> 2) + 4 * h2 + (i & 3);
                     s = key < lim ? s : -INFINITY;
+                    sacc[kb2][i] = s;
                 }
-                sacc[kb2][i] = s;
                 mx = fmaxf(mx, s);
             }
         }
-        mx = fmaxf(mx, shfl_xor_f32(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = fast_exp2(m_run - m_new);
-        m_run = m_new;
-        l_run *= alpha;
+        mx = fmaxf(mx, shfl_xor_f32(mx, 32)) * scale;
+        // Lazy rescale: the running max m_run only moves when some row's
+        // max exceeds it by more than 8 (log2 units), so exponentials stay
+        // <= 2^8 and O is rarely rescaled.
+        if (__ballot(mx > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = fast_exp2(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+            for (int dt = 0; dt < 4; ++dt) oacc[dt] *= alpha;
+        }
+        const float neg_m = -m_run;
 
         // P^T as the B operand: k-slot j of lane half h2 in step ks is key
         // kb + 16*ks + 8*(j/4) + 4*h2 + j%4.
         u32x4 pb[4];
         float psum = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks2 = 0; ks2 < 4; ++ks2) {
             float pf[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                pf[j] = fast_exp2(sacc[ks >> 1][8 * (ks & 1) + j] - m_new);
+                pf[j] = fast_exp2(fmaf(sacc[ks2 >> 1][8 * (ks2 & 1) + j], scale, neg_m));
                 psum += pf[j];
             }
-            pb[ks] = pack8(E{}, pf);
+            pb[ks2] = pack8(E{}, pf);
         }
         l_run += psum;
 
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks2 = 0; ks2 < 4; ++ks2) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const uint16_t* vrow = &Vt[(32 * dt + l32) * kVPitch + 16 * ks + 4 * h2];
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-                const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
-                oacc[dt] = mfma32x32x16(E{}, va, pb[ks], oacc[dt]);
+                u32x2 part[2];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int key = 16 * ks2 + 8 * half + v_key;
+                    const int dim = 32 * dt + v_dim;
+                    const int off = key * kRowBytes + ((((dim >> 3) ^ swz_v(key)) << 4) | ((dim & 4) << 1));
+                    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(vs + off));
+                    part[half] = __builtin_bit_cast(u32x2, r);
+                }
+                const u32x4 va = u32x4{part[0][0], part[0][1], part[1][0], part[1][1]};
+                oacc[dt] = mfma32x32x16(E{}, va, pb[ks2], oacc[dt]);
             }
         }
     }
