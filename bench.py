@@ -21,7 +21,8 @@ writes 1 GiB instead leaves ~256 MB of dirty lines whose write-back then
 competes with the measured kernel (that figure is reported alongside as
 ``ms_per_step_write_flush``).
 
-Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
+``--only copy`` times a plain 1 GiB device copy (used to calibrate the
+HBM byte counters of rocprofv3).  Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
 long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
 sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
 dense flash-attention latencies at the reference benchmark shapes.
@@ -55,7 +56,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="all", choices=["all", "decode", "prefill", "long", "mixed", "flash"])
+    ap.add_argument("--only", default="all", choices=["all", "decode", "prefill", "long", "mixed", "flash", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -80,7 +81,7 @@ class Timer:
                 self.wbuf.zero_()
             else:
                 self.rbuf.sum()
-            torch.cuda._sleep(200_000)
+            torch.cuda._sleep(1_000_000)
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record()
@@ -300,6 +301,14 @@ def main():
             mean_ms, _, _ = timer.run(fn, K, W)
             lat[str(T)] = round(mean_ms, 5)
         extra.append({"workload": "dense_flash_attention_fp16_B2_H4_D128_noncausal", "ms_by_seq_len": lat})
+
+    # ---------------- plain device copy (counter calibration, not in "all") --
+    if args.only == "copy":
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        mean_ms, _, _ = timer.run(lambda: dst.copy_(src), K, W)
+        extra.append({"workload": "device_copy_1GiB", "ms": round(mean_ms, 4),
+                      "GBs_read_plus_write": round(2 * (1 << 30) / (mean_ms * 1e-3) / 1e9, 1)})
 
     if result is None:
         result = {"metric": f"bench subset '{args.only}'", "value": None, "unit": None, "n_gpus": 1, "steps": K,

@@ -113,6 +113,25 @@ __device__ __forceinline__ f32x16 mfma32x32x16(F16, u32x4 a, u32x4 b, f32x16 c) 
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// acc + sum of the 8 packed 16-bit values in w (dot products with ones).
+// Each word is copied to a scalar before __builtin_bit_cast: applied to a
+// vector element (w[i]) directly, the cast reads element 0 for every i.
+__device__ __forceinline__ float sum8(BF16, u32x4 w, float acc) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, (uint32_t)w[i]), one, acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ float sum8(F16, u32x4 w, float acc) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, (uint32_t)w[i]), one, acc, false);
+    return acc;
+}
+
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 

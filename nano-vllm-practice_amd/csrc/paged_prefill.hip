@@ -31,6 +31,8 @@
 //  * tiles of one sequence are issued heaviest (last) first, and the work
 //    list is laid out so each XCD (workgroup id mod 8) gets a contiguous
 //    range of KV heads, keeping a head's pages in one L2.
+#include <type_traits>
+
 #include "common.h"
 #include "launch.h"
 
@@ -183,6 +185,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         kend_w = max(kend_w, __shfl_xor(kend_w, o, 64));
         kfull_w = min(kfull_w, __shfl_xor(kfull_w, o, 64));
     }
+    // Both are wave-uniform after the reductions; say so, so that the tile
+    // loop branches on scalars.
+    kend_w = __builtin_amdgcn_readfirstlane(kend_w);
+    kfull_w = __builtin_amdgcn_readfirstlane(kfull_w);
     if (lane == 0) s_kend[wave] = kend_w;
     __syncthreads();
     const int kend = max(max(s_kend[0], s_kend[1]), max(s_kend[2], s_kend[3]));
@@ -279,24 +285,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float l_run = 0.0f;
     const float scale = a.scale_log2;
 
-    const int ntiles = (kend + kKvTile - 1) / kKvTile;
-    if (ntiles > 0) {
-        fetch_table(0);
-        issue_tile(0, 0);
-    }
-    for (int it = 0; it < ntiles; ++it) {
-        const int kb = it * kKvTile;
-        const int stage = it & 1;
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile it are in LDS
-        __syncthreads();                     // ... and every wave's; stage ^ 1 is free again
-        if (it + 1 < ntiles) {
-            if (((it + 1 - tbase) & ~63) != 0) fetch_table(it + 1);
-            issue_tile(it + 1, stage ^ 1);  // in flight during this tile's math
-        }
-        if (kb >= kend_w) continue;
-        const bool need_mask = kb + kKvTile > kfull_w;
-        const uint8_t* ks = smem[stage][0];
-        const uint8_t* vs = smem[stage][1];
+    // One 64-key tile from LDS stage STAGE (a compile-time constant, so the
+    // stage offset folds into the LDS instructions' immediate offsets).
+    auto tile_math = [&](int kb, auto stage_c) {
+        constexpr int STAGE = decltype(stage_c)::value;
+        const uint8_t* ks = smem[STAGE][0];
+        const uint8_t* vs = smem[STAGE][1];
 
         // S^T blocks: keys kb + 32*kb2 + (0..31), queries = lanes (raw scores).
         f32x16 sacc[2];
@@ -312,17 +306,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
         // Accumulator i of block kb2 holds key kb + 32*kb2 + 8*(i/4) + 4*h2 + i%4.
         float mx = -INFINITY;
+        if (kb + kKvTile > kfull_w) {  // wave-uniform: tile crosses some row's limit
+            const int kr = lim - kb - 4 * h2;  // key index relative to this lane's base
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
+            for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float s = sacc[kb2][i];
-                if (need_mask) {
-                    const int key = kb + 32 * kb2 + 8 * (i >> 2) + 4 * h2 + (i & 3);
-                    s = key < lim ? s : -INFINITY;
+                for (int i = 0; i < 16; ++i) {
+                    const int rel = 32 * kb2 + 8 * (i >> 2) + (i & 3);
+                    const float s = rel < kr ? sacc[kb2][i] : -INFINITY;
                     sacc[kb2][i] = s;
+                    mx = fmaxf(mx, s);
                 }
-                mx = fmaxf(mx, s);
+            }
+        } else {
+#pragma unroll
+            for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb2][i]);
             }
         }
         mx = fmaxf(mx, shfl_xor_f32(mx, 32)) * scale;
@@ -340,20 +340,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const float neg_m = -m_run;
 
         // P^T as the B operand: k-slot j of lane half h2 in step ks is key
-        // kb + 16*ks + 8*(j/4) + 4*h2 + j%4.
+        // kb + 16*ks + 8*(j/4) + 4*h2 + j%4.  The row sum adds the rounded
+        // P values the MFMA consumes.
         u32x4 pb[4];
-        float psum = 0.0f;
 #pragma unroll
         for (int ks2 = 0; ks2 < 4; ++ks2) {
             float pf[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                pf[j] = fast_exp2(fmaf(sacc[ks2 >> 1][8 * (ks2 & 1) + j], scale, neg_m));
-                psum += pf[j];
-            }
+            for (int j = 0; j < 8; ++j) pf[j] = fast_exp2(fmaf(sacc[ks2 >> 1][8 * (ks2 & 1) + j], scale, neg_m));
             pb[ks2] = pack8(E{}, pf);
+            l_run = sum8(E{}, pb[ks2], l_run);
         }
-        l_run += psum;
 
 #pragma unroll
         for (int ks2 = 0; ks2 < 4; ++ks2) {
@@ -372,6 +369,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 oacc[dt] = mfma32x32x16(E{}, va, pb[ks2], oacc[dt]);
             }
         }
+    };
+
+    const int ntiles = (kend + kKvTile - 1) / kKvTile;
+    if (ntiles > 0) {
+        fetch_table(0);
+        issue_tile(0, 0);
+    }
+    // Loop over tiles two at a time so each half uses a constant stage.
+    auto step = [&](int it, auto stage_c) {
+        constexpr int STAGE = decltype(stage_c)::value;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile it are in LDS
+        __syncthreads();                     // ... and every wave's; the other stage is free again
+        if (it + 1 < ntiles) {
+            if (((it + 1 - tbase) & ~63) != 0) fetch_table(it + 1);
+            issue_tile(it + 1, STAGE ^ 1);  // in flight during this tile's math
+        }
+        const int kb = it * kKvTile;
+        if (kb < kend_w) tile_math(kb, stage_c);
+    };
+    for (int it = 0; it < ntiles; it += 2) {
+        step(it, std::integral_constant<int, 0>{});
+        if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
     }
 
     // ---- epilogue: O^T accumulator i of dim tile dt holds dim
