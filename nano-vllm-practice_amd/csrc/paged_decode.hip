@@ -425,21 +425,21 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
 
 template <typename E, int NREP>
 static hipError_t launch_t(DecodeArgs a, int num_seqs, hipStream_t st) {
-    // One grid of resident waves; waves_per_group of them per KV head group.
-    static int resident_wgs[64] = {0};
+    // One wave per SIMD (4 per CU), each with two pages of K and V in flight
+    // (64 KB per CU).  HBM read throughput peaks there: more resident waves
+    // queue more requests and lose bandwidth (on the 545 MB Qwen3-0.6B-shaped
+    // batch, 16 waves per CU ran at 4.85 TB/s and 4 per CU at 5.2 TB/s).
+    static int cu_count[64] = {0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    int& per_dev = resident_wgs[dev & 63];
-    if (per_dev == 0) {
-        int cus = 0, per_cu = 0;
+    int& cus = cu_count[dev & 63];
+    if (cus == 0) {
         e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         if (e != hipSuccess) return e;
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<E, NREP>, 256, 0);
-        if (e != hipSuccess) return e;
-        per_dev = cus * (per_cu > 0 ? per_cu : 1);
+        if (cus <= 0) cus = 1;
     }
-    const int total_waves = per_dev * 4;
+    const int total_waves = cus * 4;
     a.waves_per_group = total_waves / a.grid_heads > 0 ? total_waves / a.grid_heads : 1;
     const int grid = (a.waves_per_group * a.grid_heads + 3) / 4;
     hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), dim3(grid), dim3(256), 0, st, a);
