@@ -96,6 +96,33 @@ int femto_paged_attention_gemm(
     const int32_t* kv_lens, const int32_t* positions,
     void* stream);
 
+/* KV-cache write: scatter new K/V rows into the paged pools, bit-exact.
+ * k, v: (num_tokens, n_kv_heads, head_dim), element strides per token and
+ * per head (head_dim contiguous, rows 16-byte aligned).  Pools as above.
+ * Sequence b's tokens are k[cu_seqlens[b] .. cu_seqlens[b+1]) at logical
+ * positions positions[cu_seqlens[b]] + 0, 1, ...; position p goes to block
+ * kv_page_tables[b][p / 16], row p % 16.  cu_seqlens == NULL means one token
+ * per sequence (decode: num_tokens == num_seqs, token b at positions[b]).
+ * max_q_len: the longest sequence's token count (tokens beyond it are not
+ * written).  Writing stops, per sequence, at the first table column from
+ * positions[q_begin] / 16 on that holds -1, a block id outside the pool or
+ * lies past num_pages_per_seq.
+ * Replaces the per-sequence slicing loops that write the cache before the
+ * attention ops in the reference (femtovllm/models/qwen/qwen3.py:240-264 for
+ * decode, 322-366 for prefill; "TODO use kernel" at line 240).
+ * dtype: F32, F16 or BF16 (a byte copy; head_dim * element size a multiple
+ * of 16). */
+int femto_kv_cache_write(
+    int dtype,
+    const void* k, int64_t k_stride_token, int64_t k_stride_head,
+    const void* v, int64_t v_stride_token, int64_t v_stride_head,
+    void* k_pool, void* v_pool,
+    int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
+    int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+    const int32_t* cu_seqlens, int num_seqs, int num_tokens, int max_q_len,
+    const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+    void* stream);
+
 /* Dense non-causal GQA flash attention, q (B, H, Tq, D), k/v (B, KVH, Tkv, D).
  * Replaces FlashAttentionWarpCuda (csrc/flash_attention/flash_attention_warp.cu:301-376),
  * bound as _C.FlashAttentionWarpCuda (csrc/bindings.cpp:35-39, 86-89).

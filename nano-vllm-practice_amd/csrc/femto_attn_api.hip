@@ -234,6 +234,67 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
                       "paged_attention_gemm launch");
 }
 
+int femto_kv_cache_write(int dtype, const void* k, int64_t k_stride_token, int64_t k_stride_head, const void* v,
+                         int64_t v_stride_token, int64_t v_stride_head, void* k_pool, void* v_pool,
+                         int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
+                         int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+                         const int32_t* cu_seqlens, int num_seqs, int num_tokens, int max_q_len,
+                         const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq,
+                         int64_t table_stride, void* stream) {
+    g_err.clear();
+    const std::string f = "kv_cache_write";
+    if (dtype != FEMTO_F32 && dtype != FEMTO_F16 && dtype != FEMTO_BF16)
+        return fail(FEMTO_ERR_UNSUPPORTED, f + ": unsupported dtype " + std::to_string(dtype));
+    if (num_seqs < 0 || num_tokens < 0 || max_q_len < 0) return fail(FEMTO_ERR_INVALID, f + ": negative size");
+    if (num_seqs == 0 || num_tokens == 0) return FEMTO_OK;
+    if (!cu_seqlens && num_tokens != num_seqs)
+        return fail(FEMTO_ERR_INVALID, f + ": without cu_seqlens every sequence has one token (num_tokens == num_seqs)");
+    if (!cu_seqlens && max_q_len < 1) return fail(FEMTO_ERR_INVALID, f + ": max_q_len must be >= 1");
+    if (num_seqs > 65535) return fail(FEMTO_ERR_INVALID, f + ": at most 65535 sequences per call");
+    if (block_size != femto::kPage)
+        return fail(FEMTO_ERR_INVALID, f + ": block_size must be " + std::to_string(femto::kPage) + ", got " +
+                                           std::to_string(block_size));
+    const int eb = elem_bytes(dtype);
+    if (n_kv_heads <= 0 || head_dim <= 0 || (head_dim * eb) % 16 != 0)
+        return fail(FEMTO_ERR_INVALID, f + ": head_dim * element size must be a positive multiple of 16 bytes");
+    if (num_blocks < 1) return fail(FEMTO_ERR_INVALID, f + ": the pool needs at least one block");
+    if (!k || !v || !k_pool || !v_pool || !positions || !kv_page_tables)
+        return fail(FEMTO_ERR_INVALID, f + ": null pointer argument");
+    if (num_pages_per_seq < 0 || table_stride < num_pages_per_seq)
+        return fail(FEMTO_ERR_INVALID, f + ": table stride smaller than its width");
+    if (!aligned(k, 16) || !aligned(v, 16) || !aligned(k_pool, 16) || !aligned(v_pool, 16))
+        return fail(FEMTO_ERR_INVALID, f + ": k, v and the pools must be 16-byte aligned");
+    const int64_t step = 16 / eb;  // elements per 16 bytes
+    if (k_stride_token % step || k_stride_head % step || v_stride_token % step || v_stride_head % step ||
+        pool_stride_block % step || pool_stride_head % step || pool_stride_row % step)
+        return fail(FEMTO_ERR_INVALID, f + ": strides must be multiples of 16 bytes");
+
+    femto::CacheWriteArgs a{};
+    a.k = k;
+    a.v = v;
+    a.k_stride_token = k_stride_token;
+    a.k_stride_head = k_stride_head;
+    a.v_stride_token = v_stride_token;
+    a.v_stride_head = v_stride_head;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.num_blocks = num_blocks;
+    a.pool_stride_block = pool_stride_block;
+    a.pool_stride_head = pool_stride_head;
+    a.pool_stride_row = pool_stride_row;
+    a.cu_seqlens = cu_seqlens;
+    a.positions = positions;
+    a.tables = kv_page_tables;
+    a.table_stride = table_stride;
+    a.num_pages_per_seq = num_pages_per_seq;
+    a.num_seqs = num_seqs;
+    a.n_kv_heads = n_kv_heads;
+    a.row_chunks = head_dim * eb / 16;
+    a.elem_bytes = eb;
+    return hip_status(femto::launch_kv_cache_write(a, cu_seqlens ? max_q_len : 1, static_cast<hipStream_t>(stream)),
+                      "kv_cache_write launch");
+}
+
 int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int64_t q_stride_head,
                           int64_t q_stride_token, const void* k, int64_t k_stride_batch, int64_t k_stride_head,
                           int64_t k_stride_token, const void* v, int64_t v_stride_batch, int64_t v_stride_head,

@@ -1,0 +1,114 @@
+// KV-cache write: scatter the new K/V rows of a varlen batch into the
+// paged pools (num_blocks, n_kv_heads, 16, head_dim).
+//
+// Semantics follow the per-sequence slicing loops that the reference runs
+// before its attention ops (femtovllm/models/qwen/qwen3.py:240-264 for
+// decode, 322-366 for prefill): the tokens of sequence b, k[q_begin ..
+// q_end), go to logical positions p0, p0 + 1, ... with p0 =
+// positions[q_begin]; position p lands in block tables[b][p / 16], row
+// p % 16, all KV heads.  The reference walks the table from column p0 / 16
+// and stops at the first -1, so a token is written only if every column
+// from p0 / 16 up to its own holds a block id; here a column past the
+// table width or a block id outside the pool stops the walk too (the
+// reference would index out of bounds).  Rewriting a token whose block is
+// shared (the scheduler's (L-1) re-run of a cached token) stores the same
+// bytes again.  The copy is bit-exact for every element type.
+//
+// Work: workgroup (x, b) copies tokens q_begin + 16x .. + 15 of sequence b
+// (they span at most two pages).  Each thread moves 16-byte chunks; a
+// token is 2 * n_kv_heads * head_dim * element_bytes / 16 chunks (256 for
+// 8 bf16 heads of 128), so 256 threads cover one token per round.  The
+// loads of up to eight rounds are issued before their stores.
+#include "common.h"
+#include "launch.h"
+
+namespace femto {
+
+constexpr int kWriteTokens = 16;  // tokens per workgroup (one page)
+constexpr int kWriteBatch = 8;    // chunks in flight per thread
+
+__global__ __launch_bounds__(256) void kv_cache_write_kernel(CacheWriteArgs a) {
+    __shared__ int s_stop;
+    const int b = blockIdx.y;
+    int q_begin, q_end;
+    if (a.cu_seqlens) {
+        q_begin = a.cu_seqlens[b];
+        q_end = a.cu_seqlens[b + 1];
+    } else {  // decode: one token per sequence
+        q_begin = b;
+        q_end = b + 1;
+    }
+    const int t0 = q_begin + (int)blockIdx.x * kWriteTokens;
+    if (t0 >= q_end) return;
+    const int t1 = min(q_end, t0 + kWriteTokens);
+    const int p0 = a.positions[q_begin];
+    if (p0 < 0) return;
+
+    // First table column in [col0, colB] that cannot be written: -1, a
+    // block outside the pool, or past the table width.
+    const int col0 = p0 / kPage;
+    const int colA = (p0 + (t0 - q_begin)) / kPage;
+    const int colB = (p0 + (t1 - 1 - q_begin)) / kPage;
+    const int32_t* table = a.tables + (int64_t)b * a.table_stride;
+    if (threadIdx.x == 0) s_stop = 0x7fffffff;
+    __syncthreads();
+    for (int c = col0 + (int)threadIdx.x; c <= colB; c += 256) {
+        const int blk = c < a.num_pages_per_seq ? table[c] : -1;
+        if (blk < 0 || (int64_t)blk >= a.num_blocks) atomicMin(&s_stop, c);
+    }
+    __syncthreads();
+    const int stop = s_stop;
+    const int blkA = colA < stop ? table[colA] : 0;
+    const int blkB = colB < stop ? table[colB] : 0;  // colB is colA or colA + 1
+
+    const int cpr = a.row_chunks;              // 16-byte chunks per (token, head) row
+    const int half = a.n_kv_heads * cpr;       // chunks of K (then as many of V) per token
+    const int per_token = 2 * half;
+    const int total = (t1 - t0) * per_token;
+    const char* kb = static_cast<const char*>(a.k);
+    const char* vb = static_cast<const char*>(a.v);
+    char* kp = static_cast<char*>(a.k_pool);
+    char* vp = static_cast<char*>(a.v_pool);
+    for (int base = 0; base < total; base += 256 * kWriteBatch) {
+        u32x4 val[kWriteBatch];
+        char* dst[kWriteBatch];
+#pragma unroll
+        for (int j = 0; j < kWriteBatch; ++j) {
+            dst[j] = nullptr;
+            const int c = base + j * 256 + (int)threadIdx.x;
+            if (c < total) {
+                const int ti = c / per_token;
+                const int cc = c - ti * per_token;
+                const int t = t0 + ti;
+                const int p = p0 + (t - q_begin);
+                const int col = p / kPage;
+                if (col < stop) {
+                    const bool is_v = cc >= half;
+                    const int hc = is_v ? cc - half : cc;
+                    const int h = hc / cpr;
+                    const int ch = hc - h * cpr;
+                    const int blk = col == colA ? blkA : blkB;
+                    const int64_t src_el = is_v ? (int64_t)t * a.v_stride_token + (int64_t)h * a.v_stride_head
+                                                : (int64_t)t * a.k_stride_token + (int64_t)h * a.k_stride_head;
+                    const int64_t dst_el = (int64_t)blk * a.pool_stride_block + (int64_t)h * a.pool_stride_head +
+                                           (int64_t)(p % kPage) * a.pool_stride_row;
+                    val[j] = ld16((is_v ? vb : kb) + src_el * a.elem_bytes + ch * 16);
+                    dst[j] = (is_v ? vp : kp) + dst_el * a.elem_bytes + ch * 16;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kWriteBatch; ++j) {
+            if (dst[j]) st16(dst[j], val[j]);
+        }
+    }
+}
+
+hipError_t launch_kv_cache_write(const CacheWriteArgs& a, int max_q_len, hipStream_t st) {
+    if (a.num_seqs <= 0 || max_q_len <= 0) return hipSuccess;
+    const dim3 grid((max_q_len + kWriteTokens - 1) / kWriteTokens, a.num_seqs);
+    hipLaunchKernelGGL(kv_cache_write_kernel, grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace femto

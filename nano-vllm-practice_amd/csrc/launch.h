@@ -70,6 +70,29 @@ struct PrefillArgs {
     float scale_log2;
 };
 
+// KV-cache write (kv_cache_write.hip).
+struct CacheWriteArgs {
+    const void* k;  // (tokens, n_kv_heads, head_dim), any token / head strides
+    const void* v;
+    int64_t k_stride_token, k_stride_head;
+    int64_t v_stride_token, v_stride_head;
+    void* k_pool;  // (num_blocks, n_kv_heads, 16, head_dim), both pools with the same strides
+    void* v_pool;
+    int64_t num_blocks;
+    int64_t pool_stride_block, pool_stride_head, pool_stride_row;
+    const int32_t* cu_seqlens;  // null: one token per sequence (decode)
+    const int32_t* positions;   // logical position of each sequence's first token at positions[q_begin]
+    const int32_t* tables;
+    int64_t table_stride;
+    int num_pages_per_seq;
+    int num_seqs;
+    int n_kv_heads;
+    int row_chunks;  // head_dim * elem_bytes / 16
+    int elem_bytes;
+};
+
+hipError_t launch_kv_cache_write(const CacheWriteArgs& a, int max_q_len, hipStream_t st);
+
 hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st);
 hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st);
 

@@ -396,6 +396,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // ---- epilogue: O^T accumulator i of dim tile dt holds dim
     // 32*dt + 8*(i/4) + 4*h2 + i%4 of this lane's query.
     const float l_tot = l_run + shfl_xor_f32(l_run, 32);
+    const float inv_l = 1.0f / l_tot;  // 0 visible keys: 1/0 = inf, and 0 * inf = NaN as in the reference
     if (qvalid) {
         char* orow = reinterpret_cast<char*>(a.out) +
                      ((int64_t)b * a.out_stride_batch + (int64_t)h * a.out_stride_head + (int64_t)t * a.out_stride_token) * EB;
@@ -404,8 +405,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d0 = 32 * dt + 8 * g + 4 * h2;
-                const u32x2 v = pack4(E{}, oacc[dt][4 * g] / l_tot, oacc[dt][4 * g + 1] / l_tot,
-                                      oacc[dt][4 * g + 2] / l_tot, oacc[dt][4 * g + 3] / l_tot);
+                const u32x2 v = pack4(E{}, oacc[dt][4 * g] * inv_l, oacc[dt][4 * g + 1] * inv_l,
+                                      oacc[dt][4 * g + 2] * inv_l, oacc[dt][4 * g + 3] * inv_l);
                 *reinterpret_cast<u32x2*>(orow + d0 * EB) = v;
             }
         }

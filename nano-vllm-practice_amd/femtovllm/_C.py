@@ -56,6 +56,10 @@ def _load() -> ctypes.CDLL:
     lib.femto_paged_attention_gemm.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p,
     ]
+    lib.femto_kv_cache_write.restype = i
+    lib.femto_kv_cache_write.argtypes = [
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
+    ]
     lib.femto_flash_attention.restype = i
     lib.femto_flash_attention.argtypes = [
         i, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, i, i, i, i, i, i, p,
@@ -197,6 +201,56 @@ def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tabl
     )
     _raise_on(rc)
     return out
+
+
+def _kv_cache_write(k, v, k_pool, v_pool, positions, kv_page_tables, cu_seqlens=None, max_q_len=1):
+    """Scatter k, v (tokens, n_kv_heads, head_dim) into the paged pools in place."""
+    fn = "kv_cache_write"
+    for name, t in (("k", k), ("v", v), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
+    _check(k.dim() == 3 and v.dim() == 3, f"{fn}: k and v must be 3-D (tokens, n_kv_heads, head_dim)")
+    _check(tuple(k.shape) == tuple(v.shape), f"{fn}: k and v shapes differ")
+    _check(k.stride(-1) == 1 and v.stride(-1) == 1, f"{fn}: k and v must be contiguous in head_dim")
+    _check(k_pool.dim() == 4 and tuple(k_pool.shape) == tuple(v_pool.shape),
+           f"{fn}: pools must be 4-D (num_blocks, n_kv_heads, 16, head_dim) of one shape")
+    _check(k_pool.is_contiguous() and v_pool.is_contiguous(), f"{fn}: k_pool and v_pool must be contiguous")
+    _check(k.size(1) == k_pool.size(1) and k.size(2) == k_pool.size(3), f"{fn}: k/v heads or head_dim differ from the pools")
+    _check(k.dtype == v.dtype == k_pool.dtype == v_pool.dtype, f"{fn}: k, v and the pools must share a dtype")
+    _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}, got {k_pool.size(2)}")
+    _check(kv_page_tables.dtype == torch.int32 and positions.dtype == torch.int32, f"{fn}: positions and kv_page_tables must be int32")
+    _check(kv_page_tables.dim() == 2 and (kv_page_tables.size(1) <= 1 or kv_page_tables.stride(1) == 1),
+           f"{fn}: kv_page_tables must be 2-D, row-major")
+    _check(positions.is_contiguous(), f"{fn}: positions must be contiguous")
+    tensors = [("positions", positions), ("kv_page_tables", kv_page_tables)]
+    num_tokens = k.size(0)
+    num_seqs = kv_page_tables.size(0)
+    if cu_seqlens is None:
+        _check(num_tokens == num_seqs, f"{fn}: without cu_seqlens every sequence has one token")
+        _check(positions.numel() == num_seqs, f"{fn}: positions.numel() must equal the number of sequences")
+        cu_ptr = None
+    else:
+        _check(cu_seqlens.dtype == torch.int32 and cu_seqlens.is_contiguous(), f"{fn}: cu_seqlens must be contiguous int32")
+        _check(cu_seqlens.numel() - 1 == num_seqs, f"{fn}: cu_seqlens.numel()-1 must equal kv_page_tables.size(0)")
+        _check(positions.numel() == num_tokens, f"{fn}: positions.numel() must equal k.size(0)")
+        tensors.append(("cu_seqlens", cu_seqlens))
+        cu_ptr = cu_seqlens.data_ptr()
+    for name, t in tensors:
+        _check(t.device == k.device, f"{fn}: {name} must be on {k.device}")
+    dtype = _dtype_code(k, fn)
+    if num_seqs == 0 or num_tokens == 0:
+        return
+    rc = _lib.femto_kv_cache_write(
+        dtype,
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        k_pool.data_ptr(), v_pool.data_ptr(),
+        k_pool.size(0), k_pool.size(1), k_pool.size(2), k_pool.size(3),
+        k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        cu_ptr, num_seqs, num_tokens, int(max_q_len),
+        positions.data_ptr(), kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
+        _stream(k.device),
+    )
+    _raise_on(rc)
 
 
 def PagedAttentionGemvCuda(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len):

@@ -12,6 +12,11 @@ for the prefill op, ``ImplCustomKernel.TRITON`` (the reference's default)
 both select the HIP kernels; anything else raises ``NotImplementedError``
 as in the reference (ops/__init__.py:106-107, 155-156).
 
+``kv_cache_write`` has no operator counterpart in the reference: it
+replaces the per-sequence slicing loops that write the new K/V into the
+paged pools before the attention ops (femtovllm/models/qwen/qwen3.py:240-264
+for decode, 322-366 for prefill), taking the same metadata.
+
 One deliberate difference: ``q`` arrives as ``q.transpose(0, 1)`` of a
 ``(tokens, n_heads, head_dim)`` tensor (femtovllm/models/qwen/qwen3.py:270,
 372).  The reference copies it with ``.contiguous()``; the HIP kernels take
@@ -130,3 +135,34 @@ def paged_attention_gemm(
         )
     else:
         raise NotImplementedError()
+
+
+def kv_cache_write(
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_cache_pool: torch.Tensor,
+    v_cache_pool: torch.Tensor,
+    positions: torch.Tensor,
+    kv_page_tables: torch.Tensor,
+    cu_seqlens: torch.Tensor = None,
+    max_q_len: int = 1,
+):
+    """Write the new K/V rows into the paged pools (in place, bit-exact).
+
+    k, v (num_tokens, n_kv_heads, head_dim), as produced by the projections
+    (femtovllm/models/qwen/qwen3.py:231-238); pools (num_blocks, n_kv_heads,
+    16, head_dim).  Prefill: sequence b owns tokens cu_seqlens[b] ..
+    cu_seqlens[b+1] and writes them at positions[cu_seqlens[b]] + 0, 1, ...
+    (qwen3.py:322-366); decode (``cu_seqlens=None``, as in the decode
+    metadata of femtovllm/engine/model_runner.py:316-330): token b at
+    positions[b] (qwen3.py:240-264).  max_q_len is the metadata's
+    ``max_q_len``.  Position p goes to block kv_page_tables[b][p // 16], row
+    p % 16; as in the reference loops, a sequence's writes stop at the first
+    table entry that is -1 (and at block ids outside the pool).
+    """
+    for name, t in (("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"Argument '{name}' must be a CUDA tensor. Got device={t.device}")
+    k = k if k.stride(-1) == 1 else k.contiguous()
+    v = v if v.stride(-1) == 1 else v.contiguous()
+    _hip_backend._kv_cache_write(k, v, k_cache_pool, v_cache_pool, positions, kv_page_tables, cu_seqlens, max_q_len)

@@ -196,19 +196,37 @@ def dense_attention(q, k, v) -> np.ndarray:
 def cache_write(k_pool, v_pool, k_new, v_new, block_tables, cu_seqlens, positions):
     """Scatter new K/V rows into the paged pools (returns updated copies).
 
-    ``k_new``/``v_new`` are (T, KVH, D); token ``t`` of sequence ``b`` lands
-    in ``pool[block_tables[b][positions[t] // 16], :, positions[t] % 16]``,
-    which is what the per-sequence slicing loops of
-    femtovllm/models/qwen/qwen3.py:240-264 (decode) and 322-366 (prefill) do.
+    Restates the per-sequence slicing loops that write the cache before the
+    attention ops (femtovllm/models/qwen/qwen3.py:322-366 for prefill,
+    240-264 for decode).  ``k_new``/``v_new`` are (T, KVH, D).  Sequence b
+    owns tokens ``cu_seqlens[b] .. cu_seqlens[b+1]`` (``cu_seqlens=None``:
+    token b alone, the decode layout); its first token sits at logical
+    position ``p0 = positions[cu_seqlens[b]]`` and the rest follow it
+    (``remaining_cache`` advances by the tokens written, qwen3.py:330-364),
+    so token i of the sequence lands at ``p0 + i``: block
+    ``block_tables[b][(p0 + i) // 16]``, row ``(p0 + i) % 16``.  The loop
+    walks table columns from ``p0 // 16`` and breaks at the first ``-1``
+    (qwen3.py:335-338); a column past the table or a block id outside the
+    pool ends the walk the same way.
     """
     k_pool = np.array(k_pool, copy=True)
     v_pool = np.array(v_pool, copy=True)
-    page_size = k_pool.shape[2]
-    cu = [int(x) for x in cu_seqlens]
-    for b in range(len(cu) - 1):
-        for t in range(cu[b], cu[b + 1]):
-            col, row = page_slot(int(positions[t]), page_size)
-            page = int(block_tables[b][col])
-            k_pool[page, :, row] = k_new[t]
-            v_pool[page, :, row] = v_new[t]
+    num_blocks, page_size = k_pool.shape[0], k_pool.shape[2]
+    tables = [list(map(int, row)) for row in block_tables]
+    n_seq = len(tables)
+    cu = list(range(n_seq + 1)) if cu_seqlens is None else [int(x) for x in cu_seqlens]
+    for b in range(n_seq):
+        q0, q1 = cu[b], cu[b + 1]
+        if q1 <= q0:
+            continue
+        p0 = int(positions[q0])
+        if p0 < 0:
+            continue
+        for i in range(q1 - q0):
+            col, row = page_slot(p0 + i, page_size)
+            page = tables[b][col] if col < len(tables[b]) else -1
+            if page < 0 or page >= num_blocks:
+                break
+            k_pool[page, :, row] = k_new[q0 + i]
+            v_pool[page, :, row] = v_new[q0 + i]
     return k_pool, v_pool

@@ -319,6 +319,44 @@ def test_cache_write_matches_block_slice_write():
     np.testing.assert_array_equal(np.nan_to_num(got_v, nan=-7), np.nan_to_num(v_pool, nan=-7))
 
 
+def _written(pool):
+    """{(block, row): value} of the non-zero entries of a (NB, 1, 16, 1) pool."""
+    return {(int(b), int(r)): int(pool[b, 0, r, 0]) for b, _, r, _ in zip(*np.nonzero(pool))}
+
+
+@pytest.mark.parametrize("case", ["stop_at_minus_one", "past_table_width", "block_outside_pool",
+                                  "first_position_rules", "decode_layout", "shared_block_rewrite"])
+def test_cache_write_known_answers(case):
+    """Hand-computed placements of the reference loop (qwen3.py:322-366, 240-264).
+
+    Values are token ids + 1 in a (6 blocks, 1 head, 16 rows, 1 dim) pool.
+    """
+    nb = 6
+    if case == "stop_at_minus_one":      # p0 = 14: rows 14, 15 of block 3, then column 1 is -1
+        tables, cu, pos, n = [[3, -1, 5]], [0, 5], [14, 15, 16, 17, 18], 5
+        want = {(3, 14): 1, (3, 15): 2}
+    elif case == "past_table_width":     # p0 = 30: block 4 rows 14-15, block 0 rows 0-15, column 3 missing
+        tables, cu, pos, n = [[2, 4, 0]], [0, 20], list(range(30, 50)), 20
+        want = {(4, 14): 1, (4, 15): 2, **{(0, r): r + 3 for r in range(16)}}
+    elif case == "block_outside_pool":   # column 1 holds 99 >= 6 blocks: the walk stops there
+        tables, cu, pos, n = [[1, 99]], [0, 3], [15, 16, 17], 3
+        want = {(1, 15): 1}
+    elif case == "first_position_rules":  # tokens follow positions[q_begin], not their own positions
+        tables, cu, pos, n = [[5]], [0, 3], [5, 40, 2], 3
+        want = {(5, 5): 1, (5, 6): 2, (5, 7): 3}
+    elif case == "decode_layout":        # cu_seqlens=None: token b at positions[b]
+        tables, cu, pos, n = [[1, 2], [3, -1]], None, [17, 0], 2
+        want = {(2, 1): 1, (3, 0): 2}
+    else:                                # two sequences share block 2; both write row 4 of it
+        tables, cu, pos, n = [[2, 1], [2, 3]], [0, 2, 3], [3, 4, 4], 3
+        want = {(2, 3): 1, (2, 4): 3}    # the later sequence's token lands last
+    k_new = (np.arange(n, dtype=np.float64) + 1).reshape(n, 1, 1)
+    blank = np.zeros((nb, 1, 16, 1))
+    got_k, got_v = oa.cache_write(blank, blank, k_new, k_new, tables, cu, pos)
+    assert _written(got_k) == want
+    assert _written(got_v) == want
+
+
 # ---------------------------------------------------------------------------
 # Planted mistakes in the oracle are caught.
 # ---------------------------------------------------------------------------
@@ -358,3 +396,9 @@ def test_planted_missing_scale_is_caught(monkeypatch):
     monkeypatch.setattr(oa, "softmax_scale", lambda dim: 1.0)
     with pytest.raises(AssertionError):
         check_prefill_vs_sdpa()
+
+
+def test_planted_wrong_row_in_cache_write_is_caught(monkeypatch):
+    monkeypatch.setattr(oa, "page_slot", lambda j, page_size=16: (j // page_size, (j + 1) % page_size))
+    with pytest.raises(AssertionError):
+        test_cache_write_known_answers("past_table_width")
