@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|mixed|flash]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|mixed|flash|cache]
                     [--no-cpu-baseline]
 
 Headline (``value``): paged decode attention, bf16, Qwen3-0.6B attention
@@ -25,7 +25,9 @@ competes with the measured kernel (that figure is reported alongside as
 HBM byte counters of rocprofv3).  Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
 long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
 sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
-dense flash-attention latencies at the reference benchmark shapes.
+dense flash-attention latencies at the reference benchmark shapes, and the
+KV-cache write (new K/V of the 8 x 512 prefill and of a 64-sequence decode
+step scattered into the pools) in GB/s of bytes read + written.
 ``cpu_baseline``: the reference's CPU attention path (per-sequence block
 gather + torch SDPA, restated in oracle/sdpa_path.py) timed on the host in
 the workload dtype.
@@ -56,7 +58,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="all", choices=["all", "decode", "prefill", "long", "mixed", "flash", "copy"])
+    ap.add_argument("--only", default="all",
+                    choices=["all", "decode", "prefill", "long", "mixed", "flash", "cache", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -301,6 +304,38 @@ def main():
             mean_ms, _, _ = timer.run(fn, K, W)
             lat[str(T)] = round(mean_ms, 5)
         extra.append({"workload": "dense_flash_attention_fp16_B2_H4_D128_noncausal", "ms_by_seq_len": lat})
+
+    # ---------------- KV-cache write (prefill chunk and decode step) --------
+    if want("cache"):
+        w = workloads.prefill_bf16_chunked(poison=False)
+        wd = w.to(dev)
+        _, meta = wd.gemm_call(device=dev)
+        T = meta.positions.numel()
+        g = torch.Generator().manual_seed(7)
+        k_new = torch.randn((T, 8, 128), generator=g).to(torch.bfloat16).to(dev)
+        v_new = torch.randn((T, 8, 128), generator=g).to(torch.bfloat16).to(dev)
+        fn = lambda: ops.kv_cache_write(k_new, v_new, wd.k_pool, wd.v_pool, meta.positions, meta.block_tables,
+                                        cu_seqlens=meta.cu_seqlens, max_q_len=meta.max_q_len)
+        mean_ms, _, _ = timer.run(fn, K, W)
+        nbytes = 2 * 2 * k_new.numel() * k_new.element_size()  # K and V, read once and written once
+        gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        extra.append({
+            "workload": "kv_cache_write_bf16_8x512_kv8_d128", "metric": "GB/s (read + write)",
+            "value": round(gbs, 1), "ms": round(mean_ms, 5),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nbytes},
+        })
+        del wd, w
+        w = workloads.decode_bf16_qwen3_0p6b(poison=False)
+        wd = w.to(dev)
+        _, dmeta = wd.gemv_call(device=dev)
+        B = dmeta.kv_lens.numel()
+        pos = (dmeta.kv_lens - 1).contiguous()
+        kd1, vd1 = k_new[:B].contiguous(), v_new[:B].contiguous()
+        fn = lambda: ops.kv_cache_write(kd1, vd1, wd.k_pool, wd.v_pool, pos, dmeta.block_tables)
+        mean_ms, _, _ = timer.run(fn, K, W)
+        extra.append({"workload": f"kv_cache_write_bf16_decode_{B}seqs_kv8_d128", "ms": round(mean_ms, 5)})
+        del wd, w
 
     # ---------------- plain device copy (counter calibration, not in "all") --
     if args.only == "copy":
