@@ -379,18 +379,31 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
     const int t = threadIdx.x;
     char* out = reinterpret_cast<char*>(a.out);
     const int64_t o = (int64_t)h * a.out_stride_head + (int64_t)b * a.out_stride_seq + t;
-    if (a.kv_lens[b] <= 0) {
+    const int64_t sl0 = ((int64_t)b * a.n_heads + h) * a.max_slots;
+    const float* src = a.part_acc + sl0 * kDimHead + t;
+    // Every load that does not depend on another is issued first: kv_len,
+    // the slot count, (m, l) of every slot this (sequence, head) may own and
+    // the accumulators of its first kSpec slots (a sequence usually spans a
+    // few slices).  Entries past the count are stale and are masked below.
+    constexpr int kSpec = 4;
+    const int kvl = a.kv_lens[b];
+    const int count_ld = a.seq_slots[b];
+    const float m_ld = t < a.max_slots ? a.part_ml[(sl0 + t) * 2] : kEmptyMax;
+    const float l_ld = t < a.max_slots ? a.part_ml[(sl0 + t) * 2 + 1] : 0.0f;
+    float v[kSpec];
+#pragma unroll
+    for (int i = 0; i < kSpec; ++i) v[i] = i < a.max_slots ? src[(int64_t)i * kDimHead] : 0.0f;
+    if (kvl <= 0) {
         // Empty context: the reference's P.V loop never runs and its zero
         // accumulator is stored (paged_attention_gemv.cu:203-218).
         store_elem<E>(out, o, 0.0f);
         return;
     }
-    const int count = a.seq_slots[b];
-    const int64_t sl0 = ((int64_t)b * a.n_heads + h) * a.max_slots;
+    const int count = count_ld;
     // thread i < count holds slot i's (m, l); wave-reduce the max, then every
     // slot's weight exp2(m_i - M) goes to LDS.
-    const float mi = t < count ? a.part_ml[(sl0 + t) * 2] : kEmptyMax;
-    const float li = t < count ? a.part_ml[(sl0 + t) * 2 + 1] : 0.0f;
+    const float mi = t < count ? m_ld : kEmptyMax;
+    const float li = t < count ? l_ld : 0.0f;
     float M = mi;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
@@ -409,17 +422,9 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
     if (t == 0) s_l = s_ls[0] + s_ls[1];
     __syncthreads();
     float O = 0.0f;
-    const float* src = a.part_acc + sl0 * kDimHead + t;
-    int i = 0;
-    for (; i + 4 <= count; i += 4) {
-        const float v0 = src[(int64_t)(i + 0) * kDimHead], v1 = src[(int64_t)(i + 1) * kDimHead];
-        const float v2 = src[(int64_t)(i + 2) * kDimHead], v3 = src[(int64_t)(i + 3) * kDimHead];
-        O = fmaf(v0, s_w[i], O);
-        O = fmaf(v1, s_w[i + 1], O);
-        O = fmaf(v2, s_w[i + 2], O);
-        O = fmaf(v3, s_w[i + 3], O);
-    }
-    for (; i < count; ++i) O = fmaf(src[(int64_t)i * kDimHead], s_w[i], O);
+#pragma unroll
+    for (int i = 0; i < kSpec; ++i) O = fmaf(i < count ? v[i] : 0.0f, s_w[i], O);
+    for (int i = kSpec; i < count; ++i) O = fmaf(src[(int64_t)i * kDimHead], s_w[i], O);
     store_elem<E>(out, o, O / s_l);
 }
 
