@@ -27,7 +27,8 @@ long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
 sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
 dense flash-attention latencies at the reference benchmark shapes, and the
 KV-cache write (new K/V of the 8 x 512 prefill and of a 64-sequence decode
-step scattered into the pools) in GB/s of bytes read + written.
+step scattered into the pools) and the fused q/k RMSNorm + RoPE + cache write
+of the same chunk, in GB/s of bytes read + written.
 ``cpu_baseline``: the reference's CPU attention path (per-sequence block
 gather + torch SDPA, restated in oracle/sdpa_path.py) timed on the host in
 the workload dtype.
@@ -335,6 +336,33 @@ def main():
         fn = lambda: ops.kv_cache_write(kd1, vd1, wd.k_pool, wd.v_pool, pos, dmeta.block_tables)
         mean_ms, _, _ = timer.run(fn, K, W)
         extra.append({"workload": f"kv_cache_write_bf16_decode_{B}seqs_kv8_d128", "ms": round(mean_ms, 5)})
+        del wd, w
+
+        # fused prologue: q/k RMSNorm + RoPE + cache write, same 8 x 512 chunk, 16 q heads
+        from femtovllm.rope import rope_tables
+        w = workloads.prefill_bf16_chunked(poison=False)
+        wd = w.to(dev)
+        _, meta = wd.gemm_call(device=dev)
+        T = meta.positions.numel()
+        q_new = torch.randn((T, 16, 128), generator=g).to(torch.bfloat16).to(dev)
+        wq = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+        wk = (1 + 0.1 * torch.randn(128, generator=g)).to(torch.bfloat16).to(dev)
+        cos, sin = rope_tables(8192, 128, device=dev)
+        q_out = torch.empty_like(q_new)
+        fn = lambda: ops.qk_norm_rope_cache_write(q_new, k_new, v_new, wq, wk, 1e-6, cos, sin, meta.positions,
+                                                  wd.k_pool, wd.v_pool, meta.block_tables,
+                                                  cu_seqlens=meta.cu_seqlens, max_q_len=meta.max_q_len, out=q_out)
+        mean_ms, _, _ = timer.run(fn, K, W)
+        # q, k, v read once, the rope rows of every token read once, q out + k, v into the pools written once
+        esz = q_new.element_size()
+        nbytes = 2 * (q_new.numel() + 2 * k_new.numel()) * esz + 2 * T * 128 * 4
+        gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        extra.append({
+            "workload": "qk_norm_rope_cache_write_bf16_8x512_h16_kv8_d128", "metric": "GB/s (read + write)",
+            "value": round(gbs, 1), "ms": round(mean_ms, 5),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nbytes},
+        })
         del wd, w
 
     # ---------------- plain device copy (counter calibration, not in "all") --

@@ -123,6 +123,33 @@ int femto_kv_cache_write(
     const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
     void* stream);
 
+/* Fused attention prologue: per-head RMSNorm of q and k (weights q_weight,
+ * k_weight of head_dim elements, eps), rotary embedding of both at each
+ * token's position (cos/sin: fp32 tables (rope_rows, head_dim) with row
+ * stride rope_stride, as QwenRotaryEmbedding builds them), rotated q to
+ * q_out (may alias q), rotated k and raw v into the pools by the rule of
+ * femto_kv_cache_write (same cu_seqlens / positions / table arguments).
+ * Computes in fp32 and rounds each output once; a position outside the
+ * tables yields NaN rows.  head_dim must be 128.
+ * Replaces q_norm / k_norm / rotary_embd and the cache-write loops of the
+ * reference's attention layer (femtovllm/models/qwen/qwen3.py:230-264 for
+ * decode, 312-366 for prefill; RMSNorm qwen3.py:181-183, RoPE 17-138),
+ * which run as separate operators before the attention ops. */
+int femto_qk_norm_rope_cache_write(
+    int dtype,
+    const void* q, int64_t q_stride_token, int64_t q_stride_head,
+    const void* k, int64_t k_stride_token, int64_t k_stride_head,
+    const void* v, int64_t v_stride_token, int64_t v_stride_head,
+    void* q_out, int64_t q_out_stride_token, int64_t q_out_stride_head,
+    const void* q_weight, const void* k_weight, float eps,
+    const float* cos, const float* sin, int64_t rope_stride, int rope_rows,
+    void* k_pool, void* v_pool,
+    int64_t num_blocks, int n_heads, int n_kv_heads, int block_size, int head_dim,
+    int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+    const int32_t* cu_seqlens, int num_seqs, int num_tokens, int max_q_len,
+    const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+    void* stream);
+
 /* Dense non-causal GQA flash attention, q (B, H, Tq, D), k/v (B, KVH, Tkv, D).
  * Replaces FlashAttentionWarpCuda (csrc/flash_attention/flash_attention_warp.cu:301-376),
  * bound as _C.FlashAttentionWarpCuda (csrc/bindings.cpp:35-39, 86-89).

@@ -295,6 +295,91 @@ int femto_kv_cache_write(int dtype, const void* k, int64_t k_stride_token, int64
                       "kv_cache_write launch");
 }
 
+int femto_qk_norm_rope_cache_write(int dtype, const void* q, int64_t q_stride_token, int64_t q_stride_head,
+                                   const void* k, int64_t k_stride_token, int64_t k_stride_head, const void* v,
+                                   int64_t v_stride_token, int64_t v_stride_head, void* q_out,
+                                   int64_t q_out_stride_token, int64_t q_out_stride_head, const void* q_weight,
+                                   const void* k_weight, float eps, const float* cos, const float* sin,
+                                   int64_t rope_stride, int rope_rows, void* k_pool, void* v_pool,
+                                   int64_t num_blocks, int n_heads, int n_kv_heads, int block_size, int head_dim,
+                                   int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+                                   const int32_t* cu_seqlens, int num_seqs, int num_tokens, int max_q_len,
+                                   const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq,
+                                   int64_t table_stride, void* stream) {
+    g_err.clear();
+    const std::string f = "qk_norm_rope_cache_write";
+    if (dtype != FEMTO_F32 && dtype != FEMTO_F16 && dtype != FEMTO_BF16)
+        return fail(FEMTO_ERR_UNSUPPORTED, f + ": unsupported dtype " + std::to_string(dtype));
+    if (head_dim != femto::kDimHead)
+        return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be " + std::to_string(femto::kDimHead));
+    if (num_seqs < 0 || num_tokens < 0 || max_q_len < 0) return fail(FEMTO_ERR_INVALID, f + ": negative size");
+    if (num_seqs == 0 || num_tokens == 0) return FEMTO_OK;
+    if (!cu_seqlens && num_tokens != num_seqs)
+        return fail(FEMTO_ERR_INVALID, f + ": without cu_seqlens every sequence has one token (num_tokens == num_seqs)");
+    if (num_seqs > 65535) return fail(FEMTO_ERR_INVALID, f + ": at most 65535 sequences per call");
+    if (block_size != femto::kPage)
+        return fail(FEMTO_ERR_INVALID, f + ": block_size must be " + std::to_string(femto::kPage));
+    if (n_heads <= 0 || n_kv_heads <= 0) return fail(FEMTO_ERR_INVALID, f + ": head counts must be positive");
+    if (num_blocks < 1) return fail(FEMTO_ERR_INVALID, f + ": the pool needs at least one block");
+    if (!(eps >= 0.0f)) return fail(FEMTO_ERR_INVALID, f + ": eps must be >= 0");
+    if (!q || !k || !v || !q_out || !q_weight || !k_weight || !cos || !sin || !k_pool || !v_pool || !positions ||
+        !kv_page_tables)
+        return fail(FEMTO_ERR_INVALID, f + ": null pointer argument");
+    if (rope_rows < 1 || rope_stride < femto::kDimHead) return fail(FEMTO_ERR_INVALID, f + ": rope tables too small");
+    if (num_pages_per_seq < 0 || table_stride < num_pages_per_seq)
+        return fail(FEMTO_ERR_INVALID, f + ": table stride smaller than its width");
+    const int eb = elem_bytes(dtype);
+    const void* ptrs[] = {q, k, v, q_out, q_weight, k_weight, k_pool, v_pool, cos, sin};
+    for (const void* p : ptrs)
+        if (!aligned(p, 16)) return fail(FEMTO_ERR_INVALID, f + ": tensors must be 16-byte aligned");
+    const int64_t step = 16 / eb;
+    if (q_stride_token % step || q_stride_head % step || k_stride_token % step || k_stride_head % step ||
+        v_stride_token % step || v_stride_head % step || q_out_stride_token % step || q_out_stride_head % step ||
+        pool_stride_block % step || pool_stride_head % step || pool_stride_row % step || rope_stride % 4)
+        return fail(FEMTO_ERR_INVALID, f + ": strides must be multiples of 16 bytes");
+
+    femto::PrologueArgs a{};
+    femto::CacheWriteArgs& c = a.cw;
+    c.k = k;
+    c.v = v;
+    c.k_stride_token = k_stride_token;
+    c.k_stride_head = k_stride_head;
+    c.v_stride_token = v_stride_token;
+    c.v_stride_head = v_stride_head;
+    c.k_pool = k_pool;
+    c.v_pool = v_pool;
+    c.num_blocks = num_blocks;
+    c.pool_stride_block = pool_stride_block;
+    c.pool_stride_head = pool_stride_head;
+    c.pool_stride_row = pool_stride_row;
+    c.cu_seqlens = cu_seqlens;
+    c.positions = positions;
+    c.tables = kv_page_tables;
+    c.table_stride = table_stride;
+    c.num_pages_per_seq = num_pages_per_seq;
+    c.num_seqs = num_seqs;
+    c.n_kv_heads = n_kv_heads;
+    c.row_chunks = head_dim * eb / 16;
+    c.elem_bytes = eb;
+    a.q = q;
+    a.q_stride_token = q_stride_token;
+    a.q_stride_head = q_stride_head;
+    a.q_out = q_out;
+    a.q_out_stride_token = q_out_stride_token;
+    a.q_out_stride_head = q_out_stride_head;
+    a.q_weight = q_weight;
+    a.k_weight = k_weight;
+    a.eps = eps;
+    a.cos = cos;
+    a.sin = sin;
+    a.rope_stride = rope_stride;
+    a.rope_rows = rope_rows;
+    a.positions_rope = positions;
+    a.n_heads = n_heads;
+    return hip_status(femto::launch_qk_norm_rope(dtype, a, cu_seqlens ? max_q_len : 1, static_cast<hipStream_t>(stream)),
+                      "qk_norm_rope_cache_write launch");
+}
+
 int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int64_t q_stride_head,
                           int64_t q_stride_token, const void* k, int64_t k_stride_batch, int64_t k_stride_head,
                           int64_t k_stride_token, const void* v, int64_t v_stride_batch, int64_t v_stride_head,

@@ -93,6 +93,29 @@ struct CacheWriteArgs {
 
 hipError_t launch_kv_cache_write(const CacheWriteArgs& a, int max_q_len, hipStream_t st);
 
+// Fused QK-norm + RoPE + KV-cache write (qk_norm_rope.hip).  cw describes
+// the k/v sources, the pools and the placement exactly as for
+// kv_cache_write; cw.positions[q_begin] places each sequence, and
+// positions_rope[t] (the same array) is each token's rotary position.
+struct PrologueArgs {
+    CacheWriteArgs cw;
+    const void* q;  // (tokens, n_heads, 128)
+    int64_t q_stride_token, q_stride_head;
+    void* q_out;    // (tokens, n_heads, 128), may alias q
+    int64_t q_out_stride_token, q_out_stride_head;
+    const void* q_weight;  // (128,) RMSNorm weights, storage type
+    const void* k_weight;
+    float eps;
+    const float* cos;  // (rope_rows, >= 128) fp32
+    const float* sin;
+    int64_t rope_stride;
+    int rope_rows;
+    const int32_t* positions_rope;
+    int n_heads;
+};
+
+hipError_t launch_qk_norm_rope(int dtype, const PrologueArgs& a, int max_q_len, hipStream_t st);
+
 hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st);
 hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st);
 

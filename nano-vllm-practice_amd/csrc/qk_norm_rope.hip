@@ -1,0 +1,178 @@
+// Fused attention prologue: per-head RMSNorm of q and k, rotary embedding
+// of both, and the KV-cache write of the rotated k and of v.
+//
+// Reference steps (femtovllm/models/qwen/qwen3.py:230-264 decode and
+// 312-366 prefill): q = q_norm(q); k = k_norm(k) (torch.nn.RMSNorm(d_head,
+// eps), qwen3.py:181-183: x / sqrt(mean(x^2) + eps) * weight); q, k =
+// rotary_embd(., positions) (cos[p] * x + sin[p] * concat(-x2, x1),
+// QwenRotaryEmbedding.forward, qwen3.py:97-138, per-token positions); then
+// the per-sequence slicing loops write k and v into the paged pools (the
+// rule of kv_cache_write.hip: sequence b's tokens at positions[q_begin] + i,
+// stopping at the first table column that is -1, past the table width or
+// outside the pool).  Here every step runs in fp32 and each output element
+// is rounded once to the storage type (the reference rounds after the norm,
+// after the weight and after each RoPE product).  cos / sin are the
+// caller's fp32 tables (rope_rows, head_dim); a position outside them gives
+// NaN rows, where the reference's index would raise.
+//
+// Work: workgroup (x, b) takes tokens q_begin + 4x .. + 3 of sequence b.  A
+// token has H q rows, KVH k rows and KVH v rows of head_dim = 128; a DPP row
+// of 16 lanes handles one of them, lane c holding dims 8c .. 8c + 7, so the
+// sum of squares is a 16-lane DPP reduction and the RoPE partner of dim d
+// (d +- 64) sits in lane c +- 8 (one DPP row rotation).
+#include "common.h"
+#include "launch.h"
+
+namespace femto {
+
+constexpr int kProTokens = 4;  // tokens per workgroup
+
+// 8 elements at p (16 bytes for 16-bit types, 32 bytes for f32) as floats.
+__device__ __forceinline__ void load8(BF16, const char* p, float f[8]) { unpack8(BF16{}, ld16(p), f); }
+__device__ __forceinline__ void load8(F16, const char* p, float f[8]) { unpack8(F16{}, ld16(p), f); }
+__device__ __forceinline__ void load8(F32, const char* p, float f[8]) {
+    const u32x4 a = ld16(p), b = ld16(p + 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i] = __uint_as_float(a[i]);
+        f[4 + i] = __uint_as_float(b[i]);
+    }
+}
+
+__device__ __forceinline__ void store8(BF16, char* p, const float f[8]) { st16(p, pack8(BF16{}, f)); }
+__device__ __forceinline__ void store8(F16, char* p, const float f[8]) { st16(p, pack8(F16{}, f)); }
+__device__ __forceinline__ void store8(F32, char* p, const float f[8]) {
+    st16(p, u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])});
+    st16(p + 16, u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])});
+}
+
+// Raw copy of 8 elements (v rows).
+__device__ __forceinline__ void copy8(int eb, const char* src, char* dst) {
+    st16(dst, ld16(src));
+    if (eb == 4) st16(dst + 16, ld16(src + 16));
+}
+
+template <typename E>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
+    constexpr int EB = E::kBytes;
+    __shared__ int s_stop, s_blk[2];
+    const int b = blockIdx.y;
+    int q_begin, q_end;
+    if (a.cw.cu_seqlens) {
+        q_begin = a.cw.cu_seqlens[b];
+        q_end = a.cw.cu_seqlens[b + 1];
+    } else {  // decode: one token per sequence
+        q_begin = b;
+        q_end = b + 1;
+    }
+    const int t0 = q_begin + (int)blockIdx.x * kProTokens;
+    if (t0 >= q_end) return;
+    const int t1 = min(q_end, t0 + kProTokens);
+
+    // Destination pages of this workgroup's tokens (as kv_cache_write_kernel).
+    const int p0 = a.cw.positions[q_begin];
+    const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
+    const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
+    if (threadIdx.x == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
+    __syncthreads();
+    if (p0 >= 0) {
+        const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
+        for (int c = p0 / kPage + (int)threadIdx.x; c <= colB; c += 256) {
+            const int blk = c < a.cw.num_pages_per_seq ? table[c] : -1;
+            if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, c);
+            if (c == colA) s_blk[0] = blk;
+            if (c == colB) s_blk[1] = blk;
+        }
+    }
+    __syncthreads();
+    const int stop = s_stop;
+
+    const int lrow = threadIdx.x >> 4;  // DPP row of the workgroup: one (token, head row) at a time
+    const int c = threadIdx.x & 15;     // dims 8c .. 8c + 7
+    const int d0 = 8 * c;
+    float wq[8], wk[8];
+    load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
+    load8(E{}, static_cast<const char*>(a.k_weight) + d0 * EB, wk);
+
+    const int H = a.n_heads, KVH = a.cw.n_kv_heads;
+    const int R = H + 2 * KVH;  // rows per token: q heads, k heads, v heads
+    const int pairs = (t1 - t0) * R;
+    for (int pi = lrow; pi < pairs; pi += 16) {  // uniform within the DPP row
+        const int ti = pi / R;
+        const int r = pi - ti * R;
+        const int t = t0 + ti;
+        const int pc = p0 + (t - q_begin);  // cache position
+        const int col = pc / kPage;
+        const bool write_cache = p0 >= 0 && col < stop;
+        char* dst = nullptr;
+        if (r >= H && write_cache) {
+            const int h = r < H + KVH ? r - H : r - H - KVH;
+            const int blk = s_blk[col == colA ? 0 : 1];
+            const int64_t el = (int64_t)blk * a.cw.pool_stride_block + (int64_t)h * a.cw.pool_stride_head +
+                               (int64_t)(pc % kPage) * a.cw.pool_stride_row + d0;
+            dst = static_cast<char*>(r < H + KVH ? a.cw.k_pool : a.cw.v_pool) + el * EB;
+        }
+        if (r >= H + KVH) {  // v: plain copy
+            if (dst) {
+                const int h = r - H - KVH;
+                const char* src = static_cast<const char*>(a.cw.v) +
+                                  ((int64_t)t * a.cw.v_stride_token + (int64_t)h * a.cw.v_stride_head + d0) * EB;
+                copy8(EB, src, dst);
+            }
+            continue;
+        }
+        const bool is_q = r < H;
+        const int h = is_q ? r : r - H;
+        const char* src = is_q ? static_cast<const char*>(a.q) + ((int64_t)t * a.q_stride_token + (int64_t)h * a.q_stride_head + d0) * EB
+                               : static_cast<const char*>(a.cw.k) + ((int64_t)t * a.cw.k_stride_token + (int64_t)h * a.cw.k_stride_head + d0) * EB;
+        float x[8];
+        load8(E{}, src, x);
+        // RMSNorm over the 128 dims of the row.
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+        ss = row16_sum(ss);
+        const float rinv = 1.0f / sqrtf(ss * (1.0f / kDimHead) + a.eps);
+        const float* w = is_q ? wq : wk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = x[i] * rinv * w[i];
+        // RoPE at this token's position: rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] above.
+        const int pr = a.positions_rope[t];
+        const bool in_table = pr >= 0 && pr < a.rope_rows;
+        float cs[8], sn[8];
+        if (in_table) {
+            load8(F32{}, reinterpret_cast<const char*>(a.cos + (int64_t)pr * a.rope_stride + d0), cs);
+            load8(F32{}, reinterpret_cast<const char*>(a.sin + (int64_t)pr * a.rope_stride + d0), sn);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cs[i] = sn[i] = __builtin_nanf("");
+        }
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float partner = dpp_f32<0x128>(x[i]);  // lane c +- 8 (row_ror:8)
+            const float rot = c < 8 ? -partner : partner;
+            o[i] = fmaf(cs[i], x[i], sn[i] * rot);
+        }
+        if (is_q) {
+            char* qo = static_cast<char*>(a.q_out) + ((int64_t)t * a.q_out_stride_token + (int64_t)h * a.q_out_stride_head + d0) * EB;
+            store8(E{}, qo, o);
+        } else if (dst) {
+            store8(E{}, dst, o);
+        }
+    }
+}
+
+hipError_t launch_qk_norm_rope(int dtype, const PrologueArgs& a, int max_q_len, hipStream_t st) {
+    if (a.cw.num_seqs <= 0 || max_q_len <= 0) return hipSuccess;
+    const dim3 grid((max_q_len + kProTokens - 1) / kProTokens, a.cw.num_seqs);
+    switch (dtype) {
+        case kDtypeBF16: hipLaunchKernelGGL(qk_norm_rope_kernel<BF16>, grid, dim3(256), 0, st, a); break;
+        case kDtypeF16: hipLaunchKernelGGL(qk_norm_rope_kernel<F16>, grid, dim3(256), 0, st, a); break;
+        case kDtypeF32: hipLaunchKernelGGL(qk_norm_rope_kernel<F32>, grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace femto

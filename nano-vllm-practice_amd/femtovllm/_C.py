@@ -60,6 +60,11 @@ def _load() -> ctypes.CDLL:
     lib.femto_kv_cache_write.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
     ]
+    lib.femto_qk_norm_rope_cache_write.restype = i
+    lib.femto_qk_norm_rope_cache_write.argtypes = [
+        i, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i64, p, p, ctypes.c_float, p, p, i64, i,
+        p, p, i64, i, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
+    ]
     lib.femto_flash_attention.restype = i
     lib.femto_flash_attention.argtypes = [
         i, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, i, i, i, i, i, i, p,
@@ -251,6 +256,72 @@ def _kv_cache_write(k, v, k_pool, v_pool, positions, kv_page_tables, cu_seqlens=
         _stream(k.device),
     )
     _raise_on(rc)
+
+
+def _qk_norm_rope_cache_write(q, k, v, q_weight, k_weight, eps, cos, sin, positions, k_pool, v_pool,
+                              kv_page_tables, cu_seqlens=None, max_q_len=1, out=None):
+    """RMSNorm + RoPE of q and k, q to ``out``, rotated k and v into the pools; returns ``out``."""
+    fn = "qk_norm_rope_cache_write"
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_weight", q_weight), ("k_weight", k_weight),
+                    ("cos", cos), ("sin", sin), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
+        _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
+    _check(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, f"{fn}: q, k, v must be 3-D (tokens, heads, head_dim)")
+    _check(tuple(k.shape) == tuple(v.shape) and q.size(0) == k.size(0) and q.size(2) == k.size(2),
+           f"{fn}: q, k, v shapes disagree")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check(t.stride(-1) == 1, f"{fn}: {name} must be contiguous in head_dim")
+    _check(q.size(2) == kDimHead, f"{fn}: head_dim must be {kDimHead}")
+    _check(q_weight.numel() == kDimHead and k_weight.numel() == kDimHead and q_weight.is_contiguous()
+           and k_weight.is_contiguous(), f"{fn}: norm weights must be contiguous ({kDimHead},)")
+    _check(q.dtype == k.dtype == v.dtype == q_weight.dtype == k_weight.dtype == k_pool.dtype == v_pool.dtype,
+           f"{fn}: q, k, v, the norm weights and the pools must share a dtype")
+    _check(cos.dtype == torch.float32 and sin.dtype == torch.float32, f"{fn}: cos / sin tables must be float32")
+    _check(cos.dim() == 2 and tuple(cos.shape) == tuple(sin.shape) and cos.stride() == sin.stride()
+           and cos.stride(1) == 1 and cos.size(1) >= kDimHead, f"{fn}: cos / sin must be (rows, >= {kDimHead}) row-major alike")
+    _check(k_pool.dim() == 4 and tuple(k_pool.shape) == tuple(v_pool.shape) and k_pool.is_contiguous()
+           and v_pool.is_contiguous(), f"{fn}: pools must be contiguous 4-D tensors of one shape")
+    _check(k.size(1) == k_pool.size(1) and k_pool.size(3) == kDimHead, f"{fn}: k heads or head_dim differ from the pools")
+    _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}")
+    _check(q.size(1) % k.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
+    _check(positions.dtype == torch.int32 and positions.is_contiguous() and positions.device == q.device,
+           f"{fn}: positions must be a contiguous int32 tensor on {q.device}")
+    _check(kv_page_tables.dtype == torch.int32 and kv_page_tables.dim() == 2 and kv_page_tables.device == q.device
+           and (kv_page_tables.size(1) <= 1 or kv_page_tables.stride(1) == 1), f"{fn}: kv_page_tables must be 2-D row-major int32")
+    num_tokens, num_seqs = q.size(0), kv_page_tables.size(0)
+    _check(positions.numel() == num_tokens, f"{fn}: positions.numel() must equal the number of tokens")
+    if cu_seqlens is None:
+        _check(num_tokens == num_seqs, f"{fn}: without cu_seqlens every sequence has one token")
+        cu_ptr = None
+    else:
+        _check(cu_seqlens.dtype == torch.int32 and cu_seqlens.is_contiguous() and cu_seqlens.device == q.device,
+               f"{fn}: cu_seqlens must be a contiguous int32 tensor on {q.device}")
+        _check(cu_seqlens.numel() - 1 == num_seqs, f"{fn}: cu_seqlens.numel()-1 must equal kv_page_tables.size(0)")
+        cu_ptr = cu_seqlens.data_ptr()
+    if out is None:
+        out = torch.empty_like(q)
+    _check(tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype and out.stride(-1) == 1 and out.device == q.device,
+           f"{fn}: out must match q")
+    dtype = _dtype_code(q, fn)
+    if num_tokens == 0 or num_seqs == 0:
+        return out
+    rc = _lib.femto_qk_norm_rope_cache_write(
+        dtype,
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        q_weight.data_ptr(), k_weight.data_ptr(), float(eps),
+        cos.data_ptr(), sin.data_ptr(), cos.stride(0), cos.size(0),
+        k_pool.data_ptr(), v_pool.data_ptr(),
+        k_pool.size(0), q.size(1), k_pool.size(1), k_pool.size(2), k_pool.size(3),
+        k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
+        cu_ptr, num_seqs, num_tokens, int(max_q_len),
+        positions.data_ptr(), kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
+        _stream(q.device),
+    )
+    _raise_on(rc)
+    return out
 
 
 def PagedAttentionGemvCuda(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len):

@@ -12,10 +12,12 @@ for the prefill op, ``ImplCustomKernel.TRITON`` (the reference's default)
 both select the HIP kernels; anything else raises ``NotImplementedError``
 as in the reference (ops/__init__.py:106-107, 155-156).
 
-``kv_cache_write`` has no operator counterpart in the reference: it
-replaces the per-sequence slicing loops that write the new K/V into the
-paged pools before the attention ops (femtovllm/models/qwen/qwen3.py:240-264
-for decode, 322-366 for prefill), taking the same metadata.
+``kv_cache_write`` and ``qk_norm_rope_cache_write`` have no operator
+counterpart in the reference: the first replaces the per-sequence slicing
+loops that write the new K/V into the paged pools before the attention ops
+(femtovllm/models/qwen/qwen3.py:240-264 for decode, 322-366 for prefill),
+taking the same metadata; the second also fuses the q/k RMSNorm and the
+rotary embedding that precede those loops (qwen3.py:230-238, 312-320).
 
 One deliberate difference: ``q`` arrives as ``q.transpose(0, 1)`` of a
 ``(tokens, n_heads, head_dim)`` tensor (femtovllm/models/qwen/qwen3.py:270,
@@ -166,3 +168,40 @@ def kv_cache_write(
     k = k if k.stride(-1) == 1 else k.contiguous()
     v = v if v.stride(-1) == 1 else v.contiguous()
     _hip_backend._kv_cache_write(k, v, k_cache_pool, v_cache_pool, positions, kv_page_tables, cu_seqlens, max_q_len)
+
+
+def qk_norm_rope_cache_write(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_norm_weight: torch.Tensor,
+    k_norm_weight: torch.Tensor,
+    eps: float,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    positions: torch.Tensor,
+    k_cache_pool: torch.Tensor,
+    v_cache_pool: torch.Tensor,
+    kv_page_tables: torch.Tensor,
+    cu_seqlens: torch.Tensor = None,
+    max_q_len: int = 1,
+    out: torch.Tensor = None,
+):
+    """The attention layer's prologue in one kernel; returns the rotated q.
+
+    q (num_tokens, n_heads, 128), k and v (num_tokens, n_kv_heads, 128) as
+    produced by the projections; ``q_norm_weight`` / ``k_norm_weight`` and
+    ``eps`` of the layer's ``q_norm`` / ``k_norm`` RMSNorms; ``cos`` / ``sin``
+    the rotary tables of ``QwenRotaryEmbedding`` (float32, (max_seqlen,
+    128)); ``positions`` each token's position.  Computes
+    ``rotary_embd(q_norm(q))`` (returned, in ``out`` if given, which may be
+    ``q``) and ``rotary_embd(k_norm(k))``, and writes that k and v into the
+    pools exactly as :func:`kv_cache_write` (qwen3.py:230-264, 312-366).
+    Each output element is rounded once from fp32.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise ValueError(f"Argument '{name}' must be a CUDA tensor. Got device={t.device}")
+    return _hip_backend._qk_norm_rope_cache_write(q, k, v, q_norm_weight, k_norm_weight, eps, cos, sin, positions,
+                                                   k_cache_pool, v_cache_pool, kv_page_tables, cu_seqlens,
+                                                   max_q_len, out)

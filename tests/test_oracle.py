@@ -402,3 +402,68 @@ def test_planted_wrong_row_in_cache_write_is_caught(monkeypatch):
     monkeypatch.setattr(oa, "page_slot", lambda j, page_size=16: (j // page_size, (j + 1) % page_size))
     with pytest.raises(AssertionError):
         test_cache_write_known_answers("past_table_width")
+
+
+# ---------------------------------------------------------------------------
+# Prologue oracle (RMSNorm + RoPE), pinned by torch and by the complex form.
+# ---------------------------------------------------------------------------
+
+
+def test_rms_norm_matches_torch():
+    import oracle.prologue as op
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((7, 3, 128)) * 3
+    w = rng.standard_normal(128)
+    got = op.rms_norm(x, w, 1e-6)
+    want = F.rms_norm(torch.from_numpy(x), (128,), torch.from_numpy(w), 1e-6).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_rope_is_a_complex_rotation():
+    """RoPE pairs (x_i, x_{i+64}) and rotates them by theta_i = p * base**(-2i/D): as complex numbers,
+    (x_i + j x_{i+64}) * exp(j theta_i).  Checked against that form, with the tables' own theta."""
+    import oracle.prologue as op
+    rng = np.random.default_rng(42)
+    T, Hh, D = 9, 2, 128
+    x = rng.standard_normal((T, Hh, D))
+    pos = rng.integers(0, 5000, size=T)
+    cos, sin = op.rope_tables(6000, D)
+    got = op.rope(x, cos, sin, pos)
+    inv = (1.0 / 1000000.0) ** (2.0 * np.arange(D // 2) / D)
+    theta = pos[:, None] * inv[None, :]
+    z = (x[..., :64] + 1j * x[..., 64:]) * np.exp(1j * theta)[:, None, :]
+    want = np.concatenate([z.real, z.imag], axis=-1)
+    np.testing.assert_allclose(got, want, atol=5e-3)  # float32 tables vs float64 angles
+    np.testing.assert_allclose(op.rope(x, cos, sin, np.zeros(T, dtype=np.int64)), x, atol=0)  # position 0
+    pair_norm = lambda a: a[..., :64] ** 2 + a[..., 64:] ** 2
+    np.testing.assert_allclose(pair_norm(got), pair_norm(x), rtol=1e-6)
+
+
+def test_planted_wrong_rope_half_is_caught(monkeypatch):
+    import oracle.prologue as op
+
+    def bad_rope(x, cos, sin, positions):  # rotates the wrong way (sign of the swapped half)
+        x = np.asarray(x, dtype=np.float64)
+        rot = np.concatenate([x[..., 64:], -x[..., :64]], axis=-1)
+        pos = np.asarray(positions)
+        return np.asarray(cos, dtype=np.float64)[pos][:, None, :] * x + np.asarray(sin, dtype=np.float64)[pos][:, None, :] * rot
+
+    monkeypatch.setattr(op, "rope", bad_rope)
+    with pytest.raises(AssertionError):
+        test_rope_is_a_complex_rotation()
+
+
+def test_rope_tables_match_float64_angles():
+    """femtovllm.rope.rope_tables (torch, the operator's callers) and the oracle's numpy tables both
+    follow theta = p * base**(-2i/D) (qwen3.py:35-52): checked against float64 angles, within the
+    float32 angle error (~4e-7 * p) that both constructions carry."""
+    import oracle.prologue as op
+    from femtovllm.rope import rope_tables
+    P, D = 4096, 128
+    inv = (1.0 / 1000000.0) ** (2.0 * np.arange(D // 2) / D)
+    theta = np.arange(P)[:, None] * inv[None, :]
+    theta = np.concatenate([theta, theta], axis=1)
+    bound = 1e-6 + 4e-7 * np.arange(P)[:, None]
+    for cos, sin in (tuple(t.numpy() for t in rope_tables(P, D)), op.rope_tables(P, D)):
+        assert np.all(np.abs(cos - np.cos(theta)) <= bound)
+        assert np.all(np.abs(sin - np.sin(theta)) <= bound)
