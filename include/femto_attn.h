@@ -150,6 +150,24 @@ int femto_qk_norm_rope_cache_write(
     const int32_t* positions, const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
     void* stream);
 
+/* Varlen attention metadata built on the device, by the rules of the
+ * reference's ModelRunner (femtovllm/engine/model_runner.py:187-202 prefill,
+ * 283-293 decode, 46-72 block-table padding), which builds them with Python
+ * loops and one host-to-device copy per tensor.  Inputs (device, int32):
+ * num_computed[b] (= pos), num_tokens[b] (= n), the block tables in CSR form
+ * (block_offsets (num_seqs+1), block_ids).  Outputs: positions (sum n) =
+ * pos .. pos+n-1 per sequence, cu_seqlens / cu_q_tiles (num_seqs+1) prefix
+ * sums of n / ceil(n / q_tile_size), q_tile_to_seq_idx, kv_lens = pos + n,
+ * block_tables (num_seqs, table_width) padded with -1.  max_q_len: the
+ * largest n (table_width: the longest table). */
+int femto_build_varlen_metadata(
+    int num_seqs, const int32_t* num_computed, const int32_t* num_tokens,
+    const int32_t* block_offsets, const int32_t* block_ids, int table_width,
+    int q_tile_size, int max_q_len,
+    int32_t* positions, int32_t* cu_seqlens, int32_t* cu_q_tiles, int32_t* q_tile_to_seq_idx,
+    int32_t* kv_lens, int32_t* block_tables,
+    void* stream);
+
 /* Dense non-causal GQA flash attention, q (B, H, Tq, D), k/v (B, KVH, Tkv, D).
  * Replaces FlashAttentionWarpCuda (csrc/flash_attention/flash_attention_warp.cu:301-376),
  * bound as _C.FlashAttentionWarpCuda (csrc/bindings.cpp:35-39, 86-89).

@@ -23,7 +23,7 @@ INCLUDE = os.path.join(ROOT, "include")
 OUT_DIR = os.path.join(HERE, "femtovllm", "_lib")
 LIB = os.path.join(OUT_DIR, "libfemto_attn.so")
 
-SOURCES = ["femto_attn_api.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache_write.hip", "qk_norm_rope.hip"]
+SOURCES = ["femto_attn_api.hip", "paged_decode.hip", "paged_prefill.hip", "kv_cache_write.hip", "qk_norm_rope.hip", "varlen_metadata.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

@@ -380,6 +380,38 @@ int femto_qk_norm_rope_cache_write(int dtype, const void* q, int64_t q_stride_to
                       "qk_norm_rope_cache_write launch");
 }
 
+int femto_build_varlen_metadata(int num_seqs, const int32_t* num_computed, const int32_t* num_tokens,
+                                const int32_t* block_offsets, const int32_t* block_ids, int table_width,
+                                int q_tile_size, int max_q_len, int32_t* positions, int32_t* cu_seqlens,
+                                int32_t* cu_q_tiles, int32_t* q_tile_to_seq_idx, int32_t* kv_lens,
+                                int32_t* block_tables, void* stream) {
+    g_err.clear();
+    const std::string f = "build_varlen_metadata";
+    if (num_seqs < 0 || table_width < 0 || max_q_len < 0) return fail(FEMTO_ERR_INVALID, f + ": negative size");
+    if (num_seqs == 0) return FEMTO_OK;
+    if (num_seqs > 65535) return fail(FEMTO_ERR_INVALID, f + ": at most 65535 sequences per call");
+    if (q_tile_size <= 0) return fail(FEMTO_ERR_INVALID, f + ": q_tile_size must be positive");
+    if (!num_computed || !num_tokens || !block_offsets || !cu_seqlens || !cu_q_tiles || !kv_lens ||
+        (table_width > 0 && (!block_ids || !block_tables)) || (max_q_len > 0 && (!positions || !q_tile_to_seq_idx)))
+        return fail(FEMTO_ERR_INVALID, f + ": null pointer argument");
+    femto::MetadataArgs a{};
+    a.num_computed = num_computed;
+    a.num_tokens = num_tokens;
+    a.block_offsets = block_offsets;
+    a.block_ids = block_ids;
+    a.num_seqs = num_seqs;
+    a.table_width = table_width;
+    a.q_tile_size = q_tile_size;
+    a.positions = positions;
+    a.cu_seqlens = cu_seqlens;
+    a.cu_q_tiles = cu_q_tiles;
+    a.q_tile_to_seq_idx = q_tile_to_seq_idx;
+    a.kv_lens = kv_lens;
+    a.block_tables = block_tables;
+    return hip_status(femto::launch_varlen_metadata(a, max_q_len, static_cast<hipStream_t>(stream)),
+                      "build_varlen_metadata launch");
+}
+
 int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int64_t q_stride_head,
                           int64_t q_stride_token, const void* k, int64_t k_stride_batch, int64_t k_stride_head,
                           int64_t k_stride_token, const void* v, int64_t v_stride_batch, int64_t v_stride_head,

@@ -116,6 +116,23 @@ struct PrologueArgs {
 
 hipError_t launch_qk_norm_rope(int dtype, const PrologueArgs& a, int max_q_len, hipStream_t st);
 
+// Varlen metadata build (varlen_metadata.hip).
+struct MetadataArgs {
+    const int32_t* num_computed;   // (num_seqs,)
+    const int32_t* num_tokens;     // (num_seqs,)
+    const int32_t* block_offsets;  // (num_seqs + 1,) CSR offsets into block_ids
+    const int32_t* block_ids;
+    int num_seqs, table_width, q_tile_size;
+    int32_t* positions;          // (sum num_tokens,)
+    int32_t* cu_seqlens;         // (num_seqs + 1,)
+    int32_t* cu_q_tiles;         // (num_seqs + 1,)
+    int32_t* q_tile_to_seq_idx;  // (sum ceil(num_tokens / q_tile_size),)
+    int32_t* kv_lens;            // (num_seqs,)
+    int32_t* block_tables;       // (num_seqs, table_width), -1 padded
+};
+
+hipError_t launch_varlen_metadata(const MetadataArgs& a, int max_q_len, hipStream_t st);
+
 hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st);
 hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st);
 

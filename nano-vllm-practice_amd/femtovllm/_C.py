@@ -65,6 +65,8 @@ def _load() -> ctypes.CDLL:
         i, p, i64, i64, p, i64, i64, p, i64, i64, p, i64, i64, p, p, ctypes.c_float, p, p, i64, i,
         p, p, i64, i, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
     ]
+    lib.femto_build_varlen_metadata.restype = i
+    lib.femto_build_varlen_metadata.argtypes = [i, p, p, p, p, i, i, i, p, p, p, p, p, p, p]
     lib.femto_flash_attention.restype = i
     lib.femto_flash_attention.argtypes = [
         i, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, p, i64, i64, i64, i, i, i, i, i, i, p,
@@ -322,6 +324,26 @@ def _qk_norm_rope_cache_write(q, k, v, q_weight, k_weight, eps, cos, sin, positi
     )
     _raise_on(rc)
     return out
+
+
+def _build_varlen_metadata(packed, num_seqs, num_block_ids, table_width, q_tile_size, max_q_len, num_tokens_total,
+                           num_tiles_total):
+    """Run the device builder on ``packed`` = [num_computed | num_tokens | block_offsets | block_ids]
+    (int32, on the GPU); returns (positions, cu_seqlens, cu_q_tiles, q_tile_to_seq_idx, kv_lens, block_tables)."""
+    dev = packed.device
+    i32 = lambda n: torch.empty(n, dtype=torch.int32, device=dev)
+    positions, cu_seqlens, cu_q_tiles = i32(num_tokens_total), i32(num_seqs + 1), i32(num_seqs + 1)
+    tile_map, kv_lens = i32(num_tiles_total), i32(num_seqs)
+    tables = torch.empty((num_seqs, table_width), dtype=torch.int32, device=dev)
+    base = packed.data_ptr()
+    off = lambda k: base + 4 * k
+    rc = _lib.femto_build_varlen_metadata(
+        num_seqs, off(0), off(num_seqs), off(2 * num_seqs), off(3 * num_seqs + 1), table_width,
+        q_tile_size, max_q_len, positions.data_ptr(), cu_seqlens.data_ptr(), cu_q_tiles.data_ptr(),
+        tile_map.data_ptr(), kv_lens.data_ptr(), tables.data_ptr(), _stream(dev),
+    )
+    _raise_on(rc)
+    return positions, cu_seqlens, cu_q_tiles, tile_map, kv_lens, tables
 
 
 def PagedAttentionGemvCuda(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len):
