@@ -140,8 +140,8 @@ def test_decode_shape_changes_share_workspace(ops, gpu):
 
 
 def test_decode_large_batch_small_splits(ops, gpu, monkeypatch):
-    """1100 sequences split every 8 pages: a large split grid and merge grid."""
-    monkeypatch.setenv("FEMTO_DECODE_SPLIT_PAGES", "8")
+    """1100 sequences, slices of at least 4 pages: many sequences span several slices."""
+    monkeypatch.setenv("FEMTO_DECODE_MIN_CHUNK_PAGES", "4")
     rng = np.random.default_rng(19)
     lens = [int(x) for x in rng.integers(1, 300, size=1100)]
     w = workloads.make_paged_workload("many", [(L - 1, 1) for L in lens], 16, 8, seed=19)
