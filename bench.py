@@ -22,7 +22,8 @@ competes with the measured kernel (that figure is reported alongside as
 ``ms_per_step_write_flush``).
 
 ``--only copy`` times a plain 1 GiB device copy (used to calibrate the
-HBM byte counters of rocprofv3).  Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token chunks),
+HBM byte counters of rocprofv3).  Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token
+chunks, and four uneven sequences with and without the key split),
 long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
 sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
 dense flash-attention latencies at the reference benchmark shapes, and the
@@ -233,6 +234,32 @@ def main():
         extra.append({
             "workload": "chunked_prefill_bf16_8x512_prefix0-2048_h16_kv8",
             "metric": "TFLOP/s (causal-exact)", "value": round(tf, 2), "ms": round(mean_ms, 5),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops},
+        })
+        del wd, w
+
+        # Uneven batch (fewer query tiles than resident workgroups): the key
+        # split balances it; the same call without a workspace runs unsplit.
+        w = workloads.prefill_bf16_uneven(poison=False)
+        wd = w.to(dev)
+        q, meta = wd.gemm_call(device=dev)
+        fn = lambda: ops.paged_attention_gemm(q, wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len,
+                                              meta.Q_TILE_SIZE, meta.cu_q_tiles, meta.q_tile_to_seq_idx,
+                                              meta.block_tables, meta.kv_lens, meta.positions)
+        mean_ms, med_ms, _ = timer.run(fn, K, W)
+        with_ws = _C._prefill_workspace
+        _C._prefill_workspace = lambda *args: (None, 0)
+        try:
+            mean_unsplit, _, _ = timer.run(fn, K, W)
+        finally:
+            _C._prefill_workspace = with_ws
+        flops = workloads.prefill_flops(w.chunks, w.n_heads, w.head_dim)
+        tf = flops / (mean_ms * 1e-3) / 1e12
+        extra.append({
+            "workload": "chunked_prefill_bf16_uneven4_h16_kv8",
+            "metric": "TFLOP/s (causal-exact)", "value": round(tf, 2), "ms": round(mean_ms, 5),
+            "ms_without_key_split": round(mean_unsplit, 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops},
         })

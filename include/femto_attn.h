@@ -83,7 +83,14 @@ int femto_paged_attention_gemv(
  * bound as _C.PagedAttentionGemmCuda (csrc/bindings.cpp:41-50, 90-93) and
  * called by femtovllm.ops.paged_attention_gemm (femtovllm/ops/__init__.py:110-156).
  * dtype: F16 or BF16 (the reference kernels reject F32 too).  A row with
- * no visible key (kv_len == 0) is NaN, as in the reference. */
+ * no visible key (kv_len == 0) is NaN, as in the reference.
+ * workspace may be NULL.  With a workspace of at least
+ * femto_paged_attention_gemm_workspace_size() bytes (256-byte aligned,
+ * zero-filled before its first use; every call leaves it zero-filled), the
+ * query tiles of sequences much longer than the average are split over
+ * their keys and merged within the launch, so a few long sequences do not
+ * set the length of the call.  Calls that may overlap (other streams) must
+ * not share a workspace. */
 int femto_paged_attention_gemm(
     int dtype,
     const void* q, int64_t q_stride_head, int64_t q_stride_token,
@@ -94,7 +101,13 @@ int femto_paged_attention_gemm(
     const int32_t* cu_seqlens, int num_seqs, int num_tokens, int n_heads,
     const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
     const int32_t* kv_lens, const int32_t* positions,
+    void* workspace, size_t workspace_bytes,
     void* stream);
+
+/* Bytes of the optional key-split workspace of femto_paged_attention_gemm
+ * (0 for an empty call).  No counterpart in the reference, whose prefill
+ * kernels take no workspace. */
+size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads);
 
 /* KV-cache write: scatter new K/V rows into the paged pools, bit-exact.
  * k, v: (num_tokens, n_kv_heads, head_dim), element strides per token and

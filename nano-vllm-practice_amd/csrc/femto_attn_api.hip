@@ -86,6 +86,10 @@ int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
 int femto_attn_kv_len_per_page(void) { return femto::kPage; }
 int femto_attn_dim_head(void) { return femto::kDimHead; }
 
+size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
+    return femto::prefill_workspace_bytes(num_seqs, num_tokens, n_heads, n_kv_heads);
+}
+
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
     if (num_seqs <= 0 || n_heads <= 0) return 0;
     const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len);
@@ -186,7 +190,7 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
                                int64_t pool_stride_row, const int32_t* cu_seqlens, int num_seqs, int num_tokens,
                                int n_heads, const int32_t* kv_page_tables, int num_pages_per_seq,
                                int64_t table_stride, const int32_t* kv_lens, const int32_t* positions,
-                               void* stream) {
+                               void* workspace, size_t workspace_bytes, void* stream) {
     g_err.clear();
     if (dtype != FEMTO_F16 && dtype != FEMTO_BF16)
         return fail(FEMTO_ERR_UNSUPPORTED, std::string("paged_attention_gemm: not implemented for '") +
@@ -230,6 +234,16 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
     a.n_kv_heads = n_kv_heads;
     a.n_rep = n_heads / n_kv_heads;
     a.scale_log2 = scale_log2(head_dim);
+    if (workspace) {
+        const size_t need = femto::prefill_workspace_bytes(num_seqs, num_tokens, n_heads, n_kv_heads);
+        if (workspace_bytes < need || !aligned(workspace, 256))
+            return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: workspace of " + std::to_string(need) +
+                                               " bytes (256-byte aligned) required, got " +
+                                               std::to_string(workspace_bytes));
+        const size_t items = femto::prefill_work_items(num_seqs, num_tokens, n_heads, n_kv_heads);
+        a.counters = static_cast<int*>(workspace);
+        a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + femto::prefill_counter_bytes(items));
+    }
     return hip_status(femto::launch_paged_prefill(dtype, a, num_tokens, static_cast<hipStream_t>(stream)),
                       "paged_attention_gemm launch");
 }

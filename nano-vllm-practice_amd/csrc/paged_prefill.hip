@@ -30,7 +30,19 @@
 //    rarely rescaled;
 //  * tiles of one sequence are issued heaviest (last) first, and the work
 //    list is laid out so each XCD (workgroup id mod 8) gets a contiguous
-//    range of KV heads, keeping a head's pages in one L2.
+//    range of KV heads, keeping a head's pages in one L2;
+//  * key split (paged, when the caller gives a workspace): a query tile
+//    whose sequence is much longer than the average work per resident
+//    workgroup is cut into P <= 4 pieces over its key tiles, so one long
+//    sequence no longer sets the length of the whole call; only when all
+//    pieces fit in the resident workgroup slots at once.  Every piece
+//    writes its partial (m, l, O) with system-scope stores (written through
+//    to memory), waits for them, and counts itself in with a device-scope
+//    atomic; the piece that arrives last reads the others' partials with
+//    system-scope loads, merges them into its registers and writes the
+//    output.  Only the partials bypass the caches, so no cache-wide
+//    write-back or invalidate is needed.  The last piece also resets the
+//    counter and clears the slots, leaving the workspace all zeros.
 #include <type_traits>
 
 #include "common.h"
@@ -43,6 +55,7 @@ constexpr int kStages = 2;
 constexpr int kRowBytes = kDimHead * 2;                // 256
 constexpr int kTileBytes = kKvTile * kRowBytes;        // 16 KB per K or V tile
 constexpr float kEmptyMaxP = -1.0e30f;
+constexpr int kSplitTries = 4;  // key-split granularities tried (T grows by half each time)
 
 // One page of zeros: the source of every load whose block id lies outside
 // the pool, so such a page reads as zeros without a branch.
@@ -78,25 +91,68 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-__device__ __forceinline__ int block_incl_scan(int v, int* s_wsum, int& total) {
+// System-scope 16-byte accesses of the key-split partials (buffer
+// instructions with sc0 sc1: written through to memory, read past the caches).
+typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(p, (short)0, kPartSlotBytes, 0x00020000);
+}
+__device__ __forceinline__ void sys_store16(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, v), r, off, 0, 0x11);
+}
+__device__ __forceinline__ f32x4 sys_load16(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0x11));
+}
+
+// Sums of N values over the workgroup (every thread gets them); s_red holds 4 * N ints.
+template <int N>
+__device__ __forceinline__ void block_reduce_n(int (&v)[N], int* s_red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) v[k] += __shfl_xor(v[k], o, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) s_red[4 * k + wave] = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = s_red[4 * k] + s_red[4 * k + 1] + s_red[4 * k + 2] + s_red[4 * k + 3];
+    __syncthreads();
+}
+
+// Inclusive workgroup scans of two values at once (s_red holds 8 ints):
+// returns a's, and b's through incl_b; totals through total_a / total_b.
+__device__ __forceinline__ int block_incl_scan2(int a, int b, int* s_red, int& total_a, int& incl_b, int& total_b) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(v, o, 64);
-        if (lane >= o) v += u;
+        const int ua = __shfl_up(a, o, 64), ub = __shfl_up(b, o, 64);
+        if (lane >= o) {
+            a += ua;
+            b += ub;
+        }
     }
-    if (lane == 63) s_wsum[wave] = v;
+    if (lane == 63) {
+        s_red[wave] = a;
+        s_red[4 + wave] = b;
+    }
     __syncthreads();
-    int off = 0;
-    total = 0;
+    int off_a = 0, off_b = 0;
+    total_a = total_b = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const int x = s_wsum[w];
-        off += (w < wave) ? x : 0;
-        total += x;
+        const int xa = s_red[w], xb = s_red[4 + w];
+        off_a += (w < wave) ? xa : 0;
+        off_b += (w < wave) ? xb : 0;
+        total_a += xa;
+        total_b += xb;
     }
     __syncthreads();
-    return v + off;
+    incl_b = b + off_b;
+    return a + off_a;
 }
 
 template <typename E, int G, bool PAGED>
@@ -105,8 +161,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int BT = 32 * (4 / G);
     // [stage][0 = K, 1 = V][64 keys x 256 B]
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages][2][kTileBytes];
-    __shared__ int s_wsum[4];
-    __shared__ int s_seq, s_ltile;
+    __shared__ int s_red[4 * (kSplitTries + 1)];
+    __shared__ int s_seq, s_ltile, s_item0, s_old;
     __shared__ int s_kend[4];
 
     const int tid = threadIdx.x;
@@ -115,46 +171,155 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int l32 = lane & 31;
     const int h2 = lane >> 5;
 
-    // ---- work item, XCD-aware: workgroup id mod 8 selects the XCD.
-    const int per_xcd = (int)gridDim.x >> 3;
+    // ---- work item, XCD-aware: workgroup id mod 8 selects the XCD, and
+    // each XCD takes a contiguous range of the work list (KV head groups
+    // outermost, so a head's pages stay in one L2).
     const int lin = blockIdx.x;
-    const int w = (lin & 7) * per_xcd + (lin >> 3);
-    if (w >= a.total_work) return;
-    const int grp = w / a.tiles_per_group;
-    const int tile_lin = w - grp * a.tiles_per_group;
-    const int kvh = grp / a.head_groups;
-    const int hg = grp - kvh * a.head_groups;
-
+    int grp, tile_lin;
     int b, tile, q_begin, q_end, kv_len;
+    int piece = 0, npieces = 1, item = 0;  // key split of this query tile
     if constexpr (PAGED) {
-        if (tid == 0) s_seq = -1;
-        int carry = 0;
+        const int groups = a.n_kv_heads * a.head_groups;
+        bool split = a.part != nullptr;
+        // Pieces per query tile of sequence i: round(key tiles / T), where T
+        // is the estimated key tiles per resident workgroup of the whole call
+        // (query tile j of a chunk of ql tokens sees about kv_len - ql + BT (j+1)
+        // keys).  A sequence no longer than the average is never split.
+        // Per-sequence sizes, loaded once: thread t keeps sequence t (the
+        // passes below reload only for sequences past the first 256).
+        int my_q0 = 0, my_ql = 0, my_kvl = 0;
+        if (tid < a.num_seqs) {
+            my_q0 = a.cu_seqlens[tid];
+            my_ql = a.cu_seqlens[tid + 1] - my_q0;
+            my_kvl = a.kv_lens[tid];
+        }
+        auto seq_sizes = [&](int i, int& ql, int& kvl) {
+            if (i < 256) {
+                ql = my_ql;
+                kvl = my_kvl;
+            } else {
+                ql = a.cu_seqlens[i + 1] - a.cu_seqlens[i];
+                kvl = a.kv_lens[i];
+            }
+        };
+        // T: causal-estimated key tiles per resident workgroup of the call.
+        int T0 = 0;
+        if (split) {
+            for (int base = 0; base < a.num_seqs; base += 256) {
+                const int i = base + tid;
+                int est = 0;
+                if (i < a.num_seqs) {
+                    int ql, kvl;
+                    seq_sizes(i, ql, kvl);
+                    if (ql > 0 && kvl > 0) {
+                        const int mean_keys = min(kvl, max(1, kvl - ql + (ql + BT) / 2));
+                        est = ((ql + BT - 1) / BT) * ((mean_keys + kKvTile - 1) / kKvTile);
+                    }
+                }
+                int tot[1] = {est};
+                block_reduce_n(tot, s_red);
+                T0 += tot[0];
+            }
+            T0 = max(8, (int)(((int64_t)T0 * groups + a.resident - 1) / a.resident));
+        }
+        // Pieces only pay off in workgroup slots that would otherwise idle
+        // (a second round of pieces costs more than it balances): of the
+        // candidates T0, 1.5 T0, 2.25 T0, 3.375 T0 (fewer sequences split
+        // each time) the first whose pieces all fit in the resident slots at
+        // once is taken, else the call runs unsplit.
+        int Tk[kSplitTries];
+        Tk[0] = T0;
+#pragma unroll
+        for (int k = 1; k < kSplitTries; ++k) Tk[k] = Tk[k - 1] + Tk[k - 1] / 2;
+        auto pieces_of = [&](int kvl, int t) {
+            const int ub = kvl > 0 ? (kvl + kKvTile - 1) / kKvTile : 0;
+            return min(kMaxPieces, max(1, (2 * ub + t) / (2 * t)));
+        };
+        int cnt[kSplitTries + 1] = {};  // pieces per KV head group for each T; last: unsplit
         for (int base = 0; base < a.num_seqs; base += 256) {
             const int i = base + tid;
-            int nt = 0;
+            int c[kSplitTries + 1] = {};
             if (i < a.num_seqs) {
-                const int ql = a.cu_seqlens[i + 1] - a.cu_seqlens[i];
-                nt = ql > 0 ? (ql + BT - 1) / BT : 0;
+                int ql, kvl;
+                seq_sizes(i, ql, kvl);
+                const int nt = ql > 0 ? (ql + BT - 1) / BT : 0;
+#pragma unroll
+                for (int k = 0; k < kSplitTries; ++k) c[k] = split ? nt * pieces_of(kvl, Tk[k]) : nt;
+                c[kSplitTries] = nt;
             }
-            int total;
-            const int incl = block_incl_scan(nt, s_wsum, total);
-            const int excl = incl - nt;
+            block_reduce_n(c, s_red);
+#pragma unroll
+            for (int k = 0; k <= kSplitTries; ++k) cnt[k] += c[k];
+        }
+        int T = 0, total = cnt[kSplitTries];
+        if (split) {
+#pragma unroll
+            for (int k = kSplitTries - 1; k >= 0; --k) {
+                if ((int64_t)groups * cnt[k] <= a.resident) {
+                    T = Tk[k];
+                    total = cnt[k];
+                }
+            }
+        }
+        split = T > 0;
+        const int work = groups * total;
+        const int per_xcd = (work + 7) >> 3;
+        if ((lin >> 3) >= per_xcd) return;
+        const int w = (lin & 7) * per_xcd + (lin >> 3);
+        if (w >= work) return;
+        grp = w / total;
+        tile_lin = w - grp * total;
+
+        // The sequence of piece tile_lin.  Within a sequence come first the
+        // first pieces of all its query tiles (heaviest, i.e. last, tile
+        // first), then the second pieces, and so on: lengths fall smoothly
+        // along the dispatch order, so no run of long pieces queues behind
+        // one shader engine while others idle.
+        if (tid == 0) s_seq = -1;
+        int carry = 0, carry_items = 0;
+        for (int base = 0; base < a.num_seqs; base += 256) {
+            const int i = base + tid;
+            int nt = 0, pp = 1, ql = 0, kvl = 0;
+            if (i < a.num_seqs) {
+                seq_sizes(i, ql, kvl);
+                nt = ql > 0 ? (ql + BT - 1) / BT : 0;
+                pp = split ? pieces_of(kvl, T) : 1;
+            }
+            int tot, tot_items;
+            int incl_items;
+            const int incl = block_incl_scan2(nt * pp, nt, s_red, tot, incl_items, tot_items);
+            const int excl = incl - nt * pp;
             if (i < a.num_seqs && tile_lin >= carry + excl && tile_lin < carry + incl) {
                 s_seq = i;
                 s_ltile = tile_lin - carry - excl;
+                s_item0 = carry_items + incl_items - nt;
+                s_kend[0] = i < 256 ? my_q0 : a.cu_seqlens[i];  // q_begin (s_kend is rewritten below)
+                s_kend[1] = ql;
+                s_kend[2] = kvl;
+                s_kend[3] = pp;
             }
-            carry += total;
+            carry += tot;
+            carry_items += tot_items;
             if (carry > tile_lin) break;
         }
         __syncthreads();
         b = s_seq;
         if (b < 0) return;
-        q_begin = a.cu_seqlens[b];
-        q_end = a.cu_seqlens[b + 1];
-        kv_len = a.kv_lens[b];
-        const int nt = (q_end - q_begin + BT - 1) / BT;
-        tile = nt - 1 - s_ltile;  // heaviest tile of the sequence first
+        q_begin = s_kend[0];
+        q_end = q_begin + s_kend[1];
+        kv_len = s_kend[2];
+        npieces = s_kend[3];
+        const int nt = (s_kend[1] + BT - 1) / BT;
+        piece = s_ltile / nt;
+        tile = nt - 1 - (s_ltile - piece * nt);  // heaviest tile of the sequence first
+        item = grp * a.items_per_group + s_item0 + tile;
+        __syncthreads();  // s_kend is reused below
     } else {
+        const int per_xcd = (int)gridDim.x >> 3;
+        const int w = (lin & 7) * per_xcd + (lin >> 3);
+        if (w >= a.total_work) return;
+        grp = w / a.tiles_per_group;
+        tile_lin = w - grp * a.tiles_per_group;
         const int tpb = (a.q_len + BT - 1) / BT;
         b = tile_lin / tpb;
         tile = tile_lin - b * tpb;
@@ -162,6 +327,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         q_end = a.q_len;
         kv_len = a.kv_len;
     }
+    const int kvh = grp / a.head_groups;
+    const int hg = grp - kvh * a.head_groups;
 
     const int hw = wave % G;
     const int tb = wave / G;
@@ -192,6 +359,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (lane == 0) s_kend[wave] = kend_w;
     __syncthreads();
     const int kend = max(max(s_kend[0], s_kend[1]), max(s_kend[2], s_kend[3]));
+
+    // Key tiles of this piece: [t_lo, t_hi).  Pieces past the query tile's
+    // last visible key have nothing to do (and are not counted); a tile that
+    // needs a single piece is processed whole.
+    const int ntiles = (kend + kKvTile - 1) / kKvTile;
+    int t_lo = 0, t_hi = ntiles, nne = 1;
+    if (PAGED && npieces > 1) {
+        const int ub = (kv_len + kKvTile - 1) / kKvTile;
+        const int tp = (ub + npieces - 1) / npieces;
+        nne = max(1, (ntiles + tp - 1) / tp);
+        if (piece >= nne) return;
+        t_lo = piece * tp;
+        t_hi = min(ntiles, t_lo + tp);
+    }
 
     // Q rows in registers: the B operand of S^T = K . Q^T.
     u32x4 qreg[8];
@@ -371,26 +552,80 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
 
-    const int ntiles = (kend + kKvTile - 1) / kKvTile;
-    if (ntiles > 0) {
-        fetch_table(0);
-        issue_tile(0, 0);
+    if (t_hi > t_lo) {
+        fetch_table(t_lo);
+        issue_tile(t_lo, 0);
     }
     // Loop over tiles two at a time so each half uses a constant stage.
     auto step = [&](int it, auto stage_c) {
         constexpr int STAGE = decltype(stage_c)::value;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of tile it are in LDS
         __syncthreads();                     // ... and every wave's; the other stage is free again
-        if (it + 1 < ntiles) {
+        if (it + 1 < t_hi) {
             if (((it + 1 - tbase) & ~63) != 0) fetch_table(it + 1);
             issue_tile(it + 1, STAGE ^ 1);  // in flight during this tile's math
         }
         const int kb = it * kKvTile;
         if (kb < kend_w) tile_math(kb, stage_c);
     };
-    for (int it = 0; it < ntiles; it += 2) {
+    for (int it = t_lo; it < t_hi; it += 2) {
         step(it, std::integral_constant<int, 0>{});
-        if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
+        if (it + 1 < t_hi) step(it + 1, std::integral_constant<int, 1>{});
+    }
+
+    if (PAGED && nne > 1) {
+        // Partial of this piece, lane-major so each lane later reads back
+        // exactly its own values: accumulator k = 4*dt + g of lane l of wave
+        // w at 16 * ((16 w + k) * 64 + l), (m, l) at 65536 + 8 * (64 w + l).
+        uint8_t* slots = reinterpret_cast<uint8_t*>(a.part) + (int64_t)item * kMaxPieces * kPartSlotBytes;
+        {
+            const auto r = slot_rsrc(slots + (int64_t)piece * kPartSlotBytes);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    sys_store16(r, ((wave * 16 + 4 * dt + g) * 64 + lane) * 16,
+                                f32x4{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]});
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l_run)}, r,
+                                                  65536 + (wave * 64 + lane) * 8, 0, 0x11);
+        }
+        // The partial is in memory before the count goes up.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            s_old = __hip_atomic_fetch_add(a.counters + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s_old != nne - 1) return;  // another piece merges
+        if (tid == 0) __hip_atomic_exchange(a.counters + item, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::: "memory");
+        for (int q = 0; q < nne; ++q) {
+            if (q == piece) continue;
+            const auto r = slot_rsrc(slots + (int64_t)q * kPartSlotBytes);
+            const auto mlv = __builtin_amdgcn_raw_buffer_load_b64(r, 65536 + (wave * 64 + lane) * 8, 0, 0x11);
+            f32x4 v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = sys_load16(r, ((wave * 16 + k) * 64 + lane) * 16);
+            const float m_o = __uint_as_float(mlv[0]), l_o = __uint_as_float(mlv[1]);
+            const float m_new = fmaxf(m_run, m_o);
+            const float al = fast_exp2(m_run - m_new), be = fast_exp2(m_o - m_new);
+            l_run = l_run * al + l_o * be;
+            m_run = m_new;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) oacc[dt][4 * g + e] = oacc[dt][4 * g + e] * al + v[4 * dt + g][e] * be;
+        }
+        // Every partial was consumed (the merged values depend on them):
+        // clear the slots for later calls.
+        for (int q = 0; q < nne; ++q) {
+            uint8_t* sq = slots + (int64_t)q * kPartSlotBytes;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                *reinterpret_cast<f32x4*>(sq + ((wave * 16 + k) * 64 + lane) * 16) = f32x4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<u32x2*>(sq + 65536 + (wave * 64 + lane) * 8) = u32x2{0u, 0u};
+        }
     }
 
     // ---- epilogue: O^T accumulator i of dim tile dt holds dim
@@ -436,13 +671,46 @@ static hipError_t launch_dtype(int dtype, int G, const PrefillArgs& a, hipStream
     }
 }
 
+// Query tiles per (kv head, head group) are at most num_tokens / BT plus one
+// partial tile per sequence.
+static int prefill_items_per_group(int num_seqs, int num_tokens, int BT) { return (num_tokens + BT - 1) / BT + num_seqs; }
+
+size_t prefill_work_items(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
+    if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) return 0;
+    const int n_rep = n_heads / n_kv_heads;
+    const int G = pick_group(n_rep);
+    return (size_t)prefill_items_per_group(num_seqs, num_tokens, 32 * (4 / G)) * n_kv_heads * (n_rep / G);
+}
+
+size_t prefill_counter_bytes(size_t items) { return (items * sizeof(int) + 255) & ~(size_t)255; }
+
+size_t prefill_workspace_bytes(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
+    const size_t items = prefill_work_items(num_seqs, num_tokens, n_heads, n_kv_heads);
+    return items ? prefill_counter_bytes(items) + items * kMaxPieces * kPartSlotBytes : 0;
+}
+
 hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st) {
     const int G = pick_group(a.n_rep);
     const int BT = 32 * (4 / G);
     a.head_groups = a.n_rep / G;
-    a.tiles_per_group = (num_tokens + BT - 1) / BT + a.num_seqs;
+    a.items_per_group = prefill_items_per_group(a.num_seqs, num_tokens, BT);
+    a.tiles_per_group = a.items_per_group * (a.part ? kMaxPieces : 1);
     a.total_work = a.tiles_per_group * a.n_kv_heads * a.head_groups;
     if (num_tokens <= 0 || a.num_seqs <= 0) return hipSuccess;
+    if (a.part) {
+        // Two workgroups per CU are resident (LDS and register budget).
+        static int cu_count[64] = {0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        int& cus = cu_count[dev & 63];
+        if (cus == 0) {
+            e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+            if (e != hipSuccess) return e;
+            if (cus <= 0) cus = 1;
+        }
+        a.resident = 2 * cus;
+    }
     return launch_dtype<true>(dtype, G, a, st);
 }
 

@@ -54,8 +54,10 @@ def _load() -> ctypes.CDLL:
     ]
     lib.femto_paged_attention_gemm.restype = i
     lib.femto_paged_attention_gemm.argtypes = [
-        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p,
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p, sz, p,
     ]
+    lib.femto_paged_attention_gemm_workspace_size.restype = sz
+    lib.femto_paged_attention_gemm_workspace_size.argtypes = [i, i, i, i]
     lib.femto_kv_cache_write.restype = i
     lib.femto_kv_cache_write.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
@@ -111,18 +113,33 @@ def _dtype_code(t: torch.Tensor, fn: str) -> int:
 _workspaces: dict = {}
 
 
-def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_len: int):
-    nbytes = int(_lib.femto_paged_attention_gemv_workspace_size(num_seqs, n_heads, max_kv_len))
+def _cached_workspace(cache: dict, device: torch.device, nbytes: int, zero: bool):
     if nbytes == 0:
         return None, 0
     key = (device.index, _stream(device))
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+    ws = cache.get(key)
+    if ws is None or ws.numel() < nbytes + 256:
+        alloc = torch.zeros if zero else torch.empty
+        ws = alloc(nbytes + 256, dtype=torch.uint8, device=device)
+        cache[key] = ws
     ptr = ws.data_ptr()
     aligned = (ptr + 255) & ~255
     return aligned, ws.numel() - (aligned - ptr)
+
+
+def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_len: int):
+    nbytes = int(_lib.femto_paged_attention_gemv_workspace_size(num_seqs, n_heads, max_kv_len))
+    return _cached_workspace(_workspaces, device, nbytes, zero=False)
+
+
+# Key-split workspaces of the prefill kernel, one per (device, stream): the
+# kernel needs them zero-filled before the first use and leaves them so.
+_prefill_workspaces: dict = {}
+
+
+def _prefill_workspace(device: torch.device, num_seqs: int, num_tokens: int, n_heads: int, n_kv_heads: int):
+    nbytes = int(_lib.femto_paged_attention_gemm_workspace_size(num_seqs, num_tokens, n_heads, n_kv_heads))
+    return _cached_workspace(_prefill_workspaces, device, nbytes, zero=True)
 
 
 def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q):
@@ -194,6 +211,7 @@ def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tabl
     out = torch.empty((n_heads, num_tokens, dim), dtype=q.dtype, device=q.device)
     if num_seqs <= 0 or num_tokens == 0:
         return out
+    ws, ws_bytes = _prefill_workspace(q.device, num_seqs, num_tokens, n_heads, k_pool.size(1))
     rc = _lib.femto_paged_attention_gemm(
         dtype,
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -204,7 +222,7 @@ def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tabl
         cu_seqlens.data_ptr(), num_seqs, num_tokens, n_heads,
         kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
         kv_lens.data_ptr(), positions.data_ptr(),
-        _stream(q.device),
+        ws, ws_bytes, _stream(q.device),
     )
     _raise_on(rc)
     return out

@@ -226,6 +226,16 @@ def prefill_bf16_chunked(poison=True) -> PagedWorkload:
     )
 
 
+def prefill_bf16_uneven(poison=True) -> PagedWorkload:
+    """bf16 chunked prefill of four uneven sequences, H=16, KVH=8: chunks of 512,
+    512, 256 and 1024 tokens after prefixes of 3000, 200, 4000 and 100 tokens
+    (two long contexts among short ones; fewer query tiles than the GPU holds)."""
+    return make_paged_workload(
+        "prefill_bf16_uneven4", [(3000, 512), (200, 512), (4000, 256), (100, 1024)], 16, 8,
+        seed=1005, poison=poison,
+    )
+
+
 def prefill_bf16_long_llama3_8b(poison=True) -> PagedWorkload:
     """bf16 long context, Llama-3-8B attention shape: one 32768-token sequence, H=32, KVH=8.
 

@@ -1,0 +1,180 @@
+"""Key split of long query tiles in the HIP prefill kernel.
+
+With a workspace, femto_paged_attention_gemm cuts the query tiles of
+sequences much longer than the average work per resident workgroup into up
+to four pieces over their keys; the last piece to finish merges the others'
+partial softmax states within the launch.  The results must match the oracle
+(the reference's attention, paged_attention_gemm.py:83-160) and the unsplit
+kernel, and every call must leave the workspace zero-filled.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as oa
+from femtovllm import workloads
+from helpers import assert_close, np32, np64, np_tables, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _gemm(ops, q, meta, wd):
+    out = ops.paged_attention_gemm(q, wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len, meta.Q_TILE_SIZE,
+                                   meta.cu_q_tiles, meta.q_tile_to_seq_idx, meta.block_tables, meta.kv_lens,
+                                   meta.positions)
+    torch.cuda.synchronize()
+    return out
+
+
+def _unsplit(ops, q, meta, wd, monkeypatch):
+    from femtovllm import _C
+
+    with monkeypatch.context() as m:
+        m.setattr(_C, "_prefill_workspace", lambda *args: (None, 0))
+        return _gemm(ops, q, meta, wd)
+
+
+def _workspace_is_zero(device):
+    from femtovllm import _C
+
+    for key, ws in _C._prefill_workspaces.items():
+        if key[0] == device.index and int(torch.count_nonzero(ws)) != 0:
+            return False
+    return True
+
+
+def split_plan(chunks, n_heads, n_kv_heads, cus):
+    """Pieces per query tile of each sequence, by the kernel's rule: T = the
+    causal-estimated key tiles per resident workgroup (two per CU), pieces =
+    round(key tiles / T) capped at 4; while the pieces do not all fit in the
+    resident slots at once, T grows by half (three times at most), then the
+    call is not split."""
+    n_rep = n_heads // n_kv_heads
+    G = 4 if n_rep % 4 == 0 else 2 if n_rep % 2 == 0 else 1
+    BT = 32 * (4 // G)
+    groups = n_kv_heads * (n_rep // G)
+    resident = 2 * cus
+    est = 0
+    for pos, n in chunks:
+        kvl = pos + n
+        if n > 0 and kvl > 0:
+            mean_keys = min(kvl, max(1, kvl - n + (n + BT) // 2))
+            est += -(-n // BT) * -(-mean_keys // 64)
+    T = max(8, -(-est * groups // resident))
+    for _ in range(4):
+        pieces = [min(4, max(1, (2 * -(-(p + n) // 64) + T) // (2 * T))) if p + n > 0 else 1 for p, n in chunks]
+        if groups * sum(-(-n // BT) * pp for (p, n), pp in zip(chunks, pieces)) <= resident:
+            return pieces
+        T += T // 2
+    return [1] * len(chunks)
+
+
+def _cus():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def _check(ops, w, gpu, monkeypatch, rows_per_seq=6, what=""):
+    q, meta = w.gemm_call(device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    out = _gemm(ops, q, meta, wd)
+    assert _workspace_is_zero(gpu), f"workspace not cleared after {what}"
+    rows = sample_rows(meta.raw_cu_seqlens, rows_per_seq, np.random.default_rng(1))
+    want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), meta.raw_cu_seqlens, np_tables(meta),
+                            meta.raw_kv_lens, np.asarray(meta.raw_positions), rows=rows)
+    mask = np.zeros(want.shape, dtype=bool)
+    mask[:, rows] = True
+    err = assert_close(out, want, w.dtype, what, mask=mask)
+    ref = _unsplit(ops, q, meta, wd, monkeypatch)
+    assert_close(out, ref.float().cpu().numpy(), w.dtype, what + " vs unsplit")
+    return err
+
+
+# One long sequence among short ones: the long one's query tiles are split
+# into 4, 3 or 2 pieces.
+@pytest.mark.parametrize("long_prefix,pieces", [(6000, 4), (1300, 3), (800, 2)])
+def test_long_sequence_among_short(ops, gpu, monkeypatch, long_prefix, pieces):
+    chunks = [(long_prefix, 192)] + [(int(p), 64) for p in np.linspace(0, 300, 40)]
+    assert split_plan(chunks, 16, 8, _cus())[0] == pieces
+    w = workloads.make_paged_workload(f"split{long_prefix}", chunks, 16, 8, seed=long_prefix)
+    err = _check(ops, w, gpu, monkeypatch, what=f"long prefix {long_prefix}")
+    print(f"long prefix {long_prefix}: {pieces} pieces, max abs err {err:.2e}")
+
+
+def test_fresh_prompt_is_split_by_causal_length(ops, gpu, monkeypatch):
+    """A single 1024-token prompt without prefix: its late query tiles see
+    about twice the average keys and are split in two."""
+    chunks = [(0, 1024)]
+    assert split_plan(chunks, 16, 8, _cus()) == [2]
+    w = workloads.make_paged_workload("fresh", chunks, 16, 8, seed=77)
+    _check(ops, w, gpu, monkeypatch, rows_per_seq=48, what="fresh 1024-token prompt")
+
+
+def test_pieces_shrink_to_fit_resident_slots(ops, gpu, monkeypatch):
+    """Four long sequences whose first split needs more pieces than resident
+    slots: T grows until only the two longest are split (in three)."""
+    chunks = [(3000, 512), (200, 512), (4000, 256), (100, 1024)]
+    assert split_plan(chunks, 16, 8, _cus()) == [3, 1, 3, 1]
+    w = workloads.make_paged_workload("shrink", chunks, 16, 8, seed=79)
+    _check(ops, w, gpu, monkeypatch, rows_per_seq=24, what="pieces shrunk to fit")
+
+
+def test_full_gpu_call_is_not_split(ops, gpu, monkeypatch):
+    """A 2048-token prompt with 32 heads fills every resident slot with query
+    tiles already: the call runs unsplit, bit-identical to no workspace."""
+    chunks = [(0, 2048)]
+    assert split_plan(chunks, 32, 8, _cus()) == [1]
+    w = workloads.make_paged_workload("full", chunks, 32, 8, seed=78)
+    q, meta = w.gemm_call(device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    assert torch.equal(_gemm(ops, q, meta, wd), _unsplit(ops, q, meta, wd, monkeypatch))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads", [(16, 8), (32, 8), (12, 4), (6, 1), (8, 8)])
+def test_split_gqa_and_dtypes(ops, gpu, monkeypatch, dtype, heads):
+    H, KVH = heads
+    chunks = [(3000, 100), (5, 33), (40, 64), (0, 1), (200, 70)]
+    assert split_plan(chunks, H, KVH, _cus())[0] > 1
+    w = workloads.make_paged_workload("splitgqa", chunks, H, KVH, dtype=dtype, seed=H * 10 + KVH)
+    _check(ops, w, gpu, monkeypatch, what=f"split H={H} KVH={KVH} {dtype}")
+
+
+def test_arbitrary_positions_with_split(ops, gpu, monkeypatch):
+    """Positions that are not the last q_len keys: some pieces see no visible
+    key for some rows (their state is empty and must merge away)."""
+    chunks = [(4000, 96), (10, 64), (30, 64), (50, 64)]
+    assert split_plan(chunks, 16, 8, _cus())[0] == 4
+    w = workloads.make_paged_workload("splitpos", chunks, 16, 8, seed=91)
+    q, meta = w.gemm_call(device=gpu)
+    rng = np.random.default_rng(92)
+    pos = np.asarray(meta.raw_positions).copy()
+    s0, s1 = meta.raw_cu_seqlens[0], meta.raw_cu_seqlens[1]
+    pos[s0:s1] = rng.integers(0, meta.raw_kv_lens[0], size=s1 - s0)  # any visible limit inside the context
+    meta.raw_positions = [int(x) for x in pos]
+    meta.positions = torch.tensor(pos, dtype=torch.int32, device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    out = _gemm(ops, q, meta, wd)
+    assert _workspace_is_zero(gpu)
+    want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), meta.raw_cu_seqlens, np_tables(meta),
+                            meta.raw_kv_lens, pos, rows=list(range(s0, s1)))
+    mask = np.zeros(want.shape, dtype=bool)
+    mask[:, s0:s1] = True
+    assert_close(out, want, w.dtype, "arbitrary positions, split", mask=mask)
+
+
+def test_back_to_back_shapes_share_workspace(ops, gpu, monkeypatch):
+    """Calls of different shapes reuse one workspace: counters and partial
+    slots of one call must not leak into the next."""
+    cases = [
+        [(6000, 192)] + [(10, 64)] * 30,
+        [(0, 2048)],
+        [(2000, 512)] * 2 + [(0, 17)] * 50,
+        [(9000, 64), (8000, 64), (10, 32)],
+    ]
+    for i, chunks in enumerate(cases):
+        w = workloads.make_paged_workload(f"reuse{i}", chunks, 16, 8, seed=300 + i)
+        _check(ops, w, gpu, monkeypatch, rows_per_seq=4, what=f"shape sequence case {i}")
