@@ -336,53 +336,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int t = q_begin + tile * BT + tb * 32 + l32;  // this lane's query token
     const bool qvalid = t < q_end;
 
-    // Number of keys visible to this lane's query.
-    int lim;
-    if constexpr (PAGED) {
-        const int pos = qvalid ? a.positions[t] : kv_len;
-        lim = pos + 1 < kv_len ? pos + 1 : kv_len;
-        lim = lim < 0 ? 0 : lim;
-    } else {
-        lim = kv_len;
-    }
-    int kend_w = qvalid ? lim : 0;
-    int kfull_w = qvalid ? lim : 0x7fffffff;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        kend_w = max(kend_w, __shfl_xor(kend_w, o, 64));
-        kfull_w = min(kfull_w, __shfl_xor(kfull_w, o, 64));
-    }
-    // Both are wave-uniform after the reductions; say so, so that the tile
-    // loop branches on scalars.
-    kend_w = __builtin_amdgcn_readfirstlane(kend_w);
-    kfull_w = __builtin_amdgcn_readfirstlane(kfull_w);
-    if (lane == 0) s_kend[wave] = kend_w;
-    __syncthreads();
-    const int kend = max(max(s_kend[0], s_kend[1]), max(s_kend[2], s_kend[3]));
-
-    // Key tiles of this piece: [t_lo, t_hi).  Pieces past the query tile's
-    // last visible key have nothing to do (and are not counted); a tile that
-    // needs a single piece is processed whole.
-    const int ntiles = (kend + kKvTile - 1) / kKvTile;
-    int t_lo = 0, t_hi = ntiles, nne = 1;
-    if (PAGED && npieces > 1) {
-        const int ub = (kv_len + kKvTile - 1) / kKvTile;
-        const int tp = (ub + npieces - 1) / npieces;
-        nne = max(1, (ntiles + tp - 1) / tp);
-        if (piece >= nne) return;
-        t_lo = piece * tp;
-        t_hi = min(ntiles, t_lo + tp);
-    }
-
-    // Q rows in registers: the B operand of S^T = K . Q^T.
-    u32x4 qreg[8];
-    {
-        const char* qrow = reinterpret_cast<const char*>(a.q) +
-                           ((int64_t)b * a.q_stride_batch + (int64_t)h * a.q_stride_head + (int64_t)t * a.q_stride_token) * EB;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) qreg[kk] = qvalid ? ld16(qrow + (16 * kk + 8 * h2) * EB) : u32x4{0, 0, 0, 0};
-    }
-
     // ---- KV staging: wave w copies page w of each tile (16 keys x 256 B of
     // K and of V) with 4 + 4 direct-to-LDS loads; in load j, lane i writes
     // LDS row 16w + 4j + i/16, chunk position i%16, and so fetches logical
@@ -449,6 +402,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             lds_dma16(vp, (uint32_t)(row * rs_v + voff[j]), vd + j * 1024);
         }
     };
+
+    // The first tile of this piece does not depend on the causal limits:
+    // its block ids and its copy into LDS go out now, while the positions
+    // load below is in flight.  Every exit before the tile loop waits for
+    // this copy (it must not land in LDS after the workgroup has left).
+    int t_first = 0;
+    if (PAGED && npieces > 1) {
+        const int ub = (kv_len + kKvTile - 1) / kKvTile;
+        t_first = piece * ((ub + npieces - 1) / npieces);
+    }
+    const bool first_issued = t_first * kKvTile < kv_len;
+    if (first_issued) {
+        fetch_table(t_first);
+        issue_tile(t_first, 0);
+    }
+
+    // Number of keys visible to this lane's query.
+    int lim;
+    if constexpr (PAGED) {
+        const int pos = qvalid ? a.positions[t] : kv_len;
+        lim = pos + 1 < kv_len ? pos + 1 : kv_len;
+        lim = lim < 0 ? 0 : lim;
+    } else {
+        lim = kv_len;
+    }
+    int kend_w = qvalid ? lim : 0;
+    int kfull_w = qvalid ? lim : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        kend_w = max(kend_w, __shfl_xor(kend_w, o, 64));
+        kfull_w = min(kfull_w, __shfl_xor(kfull_w, o, 64));
+    }
+    // Both are wave-uniform after the reductions; say so, so that the tile
+    // loop branches on scalars.
+    kend_w = __builtin_amdgcn_readfirstlane(kend_w);
+    kfull_w = __builtin_amdgcn_readfirstlane(kfull_w);
+    if (lane == 0) s_kend[wave] = kend_w;
+    __syncthreads();
+    const int kend = max(max(s_kend[0], s_kend[1]), max(s_kend[2], s_kend[3]));
+
+    // Key tiles of this piece: [t_lo, t_hi).  Pieces past the query tile's
+    // last visible key have nothing to do (and are not counted); a tile that
+    // needs a single piece is processed whole.
+    const int ntiles = (kend + kKvTile - 1) / kKvTile;
+    int t_lo = 0, t_hi = ntiles, nne = 1;
+    if (PAGED && npieces > 1) {
+        const int ub = (kv_len + kKvTile - 1) / kKvTile;
+        const int tp = (ub + npieces - 1) / npieces;
+        nne = max(1, (ntiles + tp - 1) / tp);
+        if (piece >= nne) {
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the first tile's copy has landed
+            return;
+        }
+        t_lo = piece * tp;
+        t_hi = min(ntiles, t_lo + tp);
+    }
+    if (t_hi <= t_lo) __builtin_amdgcn_s_waitcnt(0x0f70);  // no tile: only wait for the copy
+
+    // Q rows in registers: the B operand of S^T = K . Q^T.
+    u32x4 qreg[8];
+    {
+        const char* qrow = reinterpret_cast<const char*>(a.q) +
+                           ((int64_t)b * a.q_stride_batch + (int64_t)h * a.q_stride_head + (int64_t)t * a.q_stride_token) * EB;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) qreg[kk] = qvalid ? ld16(qrow + (16 * kk + 8 * h2) * EB) : u32x4{0, 0, 0, 0};
+    }
 
     // Per-lane constant parts of the LDS operand addresses.
     const int k_rd = l32 * kRowBytes;  // K row l32 (+ 32 * kb2 rows)
@@ -552,10 +571,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     };
 
-    if (t_hi > t_lo) {
-        fetch_table(t_lo);
-        issue_tile(t_lo, 0);
-    }
     // Loop over tiles two at a time so each half uses a constant stage.
     auto step = [&](int it, auto stage_c) {
         constexpr int STAGE = decltype(stage_c)::value;
