@@ -178,3 +178,33 @@ def test_back_to_back_shapes_share_workspace(ops, gpu, monkeypatch):
     for i, chunks in enumerate(cases):
         w = workloads.make_paged_workload(f"reuse{i}", chunks, 16, 8, seed=300 + i)
         _check(ops, w, gpu, monkeypatch, rows_per_seq=4, what=f"shape sequence case {i}")
+
+
+@pytest.mark.parametrize("num_seqs", [300, 700])
+def test_many_sequences(ops, gpu, monkeypatch, num_seqs):
+    """More sequences than one workgroup pass covers (256): the kernel's
+    per-sequence passes run over several chunks, and the work item of a
+    query tile past the first 256 sequences is found in a later chunk.  A
+    few long contexts among them are split when their pieces fit."""
+    rng = np.random.default_rng(num_seqs)
+    chunks = []
+    for i in range(num_seqs):
+        if i % 97 == 5:
+            chunks.append((int(rng.integers(3000, 6000)), int(rng.integers(64, 200))))  # long context
+        elif i % 3 == 0:
+            chunks.append((int(rng.integers(0, 400)), 1))  # decode token
+        else:
+            chunks.append((int(rng.integers(0, 300)), int(rng.integers(1, 40))))
+    w = workloads.make_paged_workload(f"many{num_seqs}", chunks, 16, 8, seed=num_seqs)
+    _check(ops, w, gpu, monkeypatch, rows_per_seq=1, what=f"{num_seqs} sequences")
+
+
+def test_many_sequences_with_one_split(ops, gpu, monkeypatch):
+    """300 sequences of one decode token each and one long chunk at the end,
+    one KV head (so the pieces fit the resident slots): the long sequence
+    (index 300) is split and lives in the second chunk of the kernel's
+    per-sequence passes."""
+    chunks = [(int(p), 1) for p in np.linspace(10, 500, 300)] + [(8000, 128)]
+    assert split_plan(chunks, 2, 1, _cus())[-1] == 4
+    w = workloads.make_paged_workload("many_split", chunks, 2, 1, seed=261)
+    _check(ops, w, gpu, monkeypatch, rows_per_seq=2, what="300 decode + 1 long")
