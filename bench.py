@@ -25,8 +25,10 @@ competes with the measured kernel (that figure is reported alongside as
 HBM byte counters of rocprofv3).  Also reported (``extra``): chunked prefill TFLOP/s (8 x 512-token
 chunks, and four uneven sequences with and without the key split),
 long-context prefill (Llama-3-8B shape, 16 x 2048-token chunks of a 32k
-sequence), the unified mixed batch (Qwen3-8B shape, both routes) and the
-dense flash-attention latencies at the reference benchmark shapes, and the
+sequence, and one GPU's 4-head / 1-KV-head share of it under 8-way tensor
+parallelism, with and without the key split), the unified mixed batch
+(Qwen3-8B shape, both routes), the dense flash-attention latencies at the
+reference benchmark shapes and its TFLOP/s at the long-context chunk shapes, and the
 KV-cache write (new K/V of the 8 x 512 prefill and of a 64-sequence decode
 step scattered into the pools) and the fused q/k RMSNorm + RoPE + cache write
 of the same chunk, in GB/s of bytes read + written.
@@ -292,6 +294,37 @@ def main():
         })
         del wd, w, calls
 
+        # One GPU's share of the same job under 8-way tensor parallelism (4 query
+        # heads, 1 KV head): 64 query tiles per chunk for 512 resident workgroups,
+        # the case the key split is for; also timed without it.
+        w = workloads.prefill_bf16_long_tp8_share(poison=False)
+        wd = w.to(dev)
+        calls = [workloads.long_context_chunk(wd, c, device=dev) for c in range(16)]
+
+        def fn():
+            for q, meta in calls:
+                ops.paged_attention_gemm(q, wd.k_pool, wd.v_pool, meta.cu_seqlens, meta.max_q_len, meta.Q_TILE_SIZE,
+                                         meta.cu_q_tiles, meta.q_tile_to_seq_idx, meta.block_tables, meta.kv_lens,
+                                         meta.positions)
+
+        mean_ms, _, _ = timer.run(fn, steps, max(1, W // 2))
+        with_ws = _C._prefill_workspace
+        _C._prefill_workspace = lambda *args: (None, 0)
+        try:
+            mean_unsplit, _, _ = timer.run(fn, steps, max(1, W // 2))
+        finally:
+            _C._prefill_workspace = with_ws
+        flops = workloads.prefill_flops([(2048 * c, 2048) for c in range(16)], 4, 128)
+        tf = flops / (mean_ms * 1e-3) / 1e12
+        extra.append({
+            "workload": "long_context_prefill_bf16_llama3_8b_32k_tp8_share_h4_kv1",
+            "metric": "TFLOP/s (causal-exact, 16 calls)", "value": round(tf, 2), "ms": round(mean_ms, 4),
+            "ms_without_key_split": round(mean_unsplit, 4),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": flops},
+        })
+        del wd, w, calls
+
     # ---------------- unified mixed batch ---------------------------------
     if want("mixed"):
         w = workloads.mixed_bf16_qwen3_8b(poison=False)
@@ -332,6 +365,22 @@ def main():
             mean_ms, _, _ = timer.run(fn, K, W)
             lat[str(T)] = round(mean_ms, 5)
         extra.append({"workload": "dense_flash_attention_fp16_B2_H4_D128_noncausal", "ms_by_seq_len": lat})
+
+        # The dense entry at the long-context chunk shapes (q: 2048 tokens x 32
+        # heads, k/v: 8 KV heads), bf16, non-causal: FLOPs = 4 B H Tq Tkv D.
+        tf_by_kv = {}
+        for tkv in (2048, 8192, 32768):
+            g = torch.Generator().manual_seed(tkv)
+            q = torch.randn((1, 32, 2048, 128), generator=g).to(torch.bfloat16).to(dev)
+            k = torch.randn((1, 8, tkv, 128), generator=g).to(torch.bfloat16).to(dev)
+            v = torch.randn((1, 8, tkv, 128), generator=g).to(torch.bfloat16).to(dev)
+            fn = lambda: _C.FlashAttentionWarpCuda(q, k, v)
+            mean_ms, _, _ = timer.run(fn, K, W)
+            tf_by_kv[str(tkv)] = round(4 * 32 * 2048 * tkv * 128 / (mean_ms * 1e-3) / 1e12, 1)
+            del q, k, v
+        extra.append({"workload": "dense_flash_attention_bf16_B1_H32_KV8_Tq2048_noncausal",
+                      "metric": "TFLOP/s by kv length", "tflops_by_kv_len": tf_by_kv,
+                      "peak": BF16_PEAK_TFLOPS})
 
     # ---------------- KV-cache write (prefill chunk and decode step) --------
     if want("cache"):

@@ -87,7 +87,10 @@ int femto_attn_kv_len_per_page(void) { return femto::kPage; }
 int femto_attn_dim_head(void) { return femto::kDimHead; }
 
 size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
-    return femto::prefill_workspace_bytes(num_seqs, num_tokens, n_heads, n_kv_heads);
+    if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads) return 0;
+    int resident = 0;
+    if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
+    return femto::prefill_workspace_bytes(resident);
 }
 
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
@@ -235,14 +238,16 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
     a.n_rep = n_heads / n_kv_heads;
     a.scale_log2 = scale_log2(head_dim);
     if (workspace) {
-        const size_t need = femto::prefill_workspace_bytes(num_seqs, num_tokens, n_heads, n_kv_heads);
+        int resident = 0;
+        rc = hip_status(femto::prefill_resident_workgroups(resident), "paged_attention_gemm: device query");
+        if (rc != FEMTO_OK) return rc;
+        const size_t need = femto::prefill_workspace_bytes(resident);
         if (workspace_bytes < need || !aligned(workspace, 256))
             return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: workspace of " + std::to_string(need) +
                                                " bytes (256-byte aligned) required, got " +
                                                std::to_string(workspace_bytes));
-        const size_t items = femto::prefill_work_items(num_seqs, num_tokens, n_heads, n_kv_heads);
         a.counters = static_cast<int*>(workspace);
-        a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + femto::prefill_counter_bytes(items));
+        a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + femto::prefill_counter_bytes(resident));
     }
     return hip_status(femto::launch_paged_prefill(dtype, a, num_tokens, static_cast<hipStream_t>(stream)),
                       "paged_attention_gemm launch");

@@ -69,19 +69,19 @@ struct PrefillArgs {
     int total_work;       // tiles_per_group * n_kv_heads * head_groups (grid size)
     float scale_log2;
     // Key split of long query tiles (paged only; part == nullptr: none).
-    float* part;          // kMaxPieces partial slots of kPartSlotBytes per query tile
-    int* counters;        // finished pieces per query tile
+    float* part;          // one partial slot of kPartSlotBytes per resident workgroup
+    int* counters;        // one arrival counter per resident workgroup
     int items_per_group;  // upper bound on query tiles per (kv head, head group)
     int resident;         // workgroups the GPU holds at once
 };
 
 // Key split: at most kMaxPieces pieces per query tile, each leaving a
 // partial (m, l, O) slot: 4 waves x 64 lanes x (64 accumulators + m, l).
-constexpr int kMaxPieces = 4;
+constexpr int kMaxPieces = 8;
 constexpr int kPartSlotBytes = 4 * 64 * 64 * 4 + 4 * 64 * 8;
-size_t prefill_work_items(int num_seqs, int num_tokens, int n_heads, int n_kv_heads);
-size_t prefill_counter_bytes(size_t items);
-size_t prefill_workspace_bytes(int num_seqs, int num_tokens, int n_heads, int n_kv_heads);
+hipError_t prefill_resident_workgroups(int& resident);
+size_t prefill_counter_bytes(int resident);
+size_t prefill_workspace_bytes(int resident);
 
 // KV-cache write (kv_cache_write.hip).
 struct CacheWriteArgs {

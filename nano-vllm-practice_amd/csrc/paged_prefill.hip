@@ -123,36 +123,27 @@ __device__ __forceinline__ void block_reduce_n(int (&v)[N], int* s_red) {
     __syncthreads();
 }
 
-// Inclusive workgroup scans of two values at once (s_red holds 8 ints):
-// returns a's, and b's through incl_b; totals through total_a / total_b.
-__device__ __forceinline__ int block_incl_scan2(int a, int b, int* s_red, int& total_a, int& incl_b, int& total_b) {
+// Inclusive workgroup scan (every thread gets its prefix and the total);
+// s_red holds 4 ints.
+__device__ __forceinline__ int block_incl_scan(int v, int* s_red, int& total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        const int ua = __shfl_up(a, o, 64), ub = __shfl_up(b, o, 64);
-        if (lane >= o) {
-            a += ua;
-            b += ub;
-        }
+        const int u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
     }
-    if (lane == 63) {
-        s_red[wave] = a;
-        s_red[4 + wave] = b;
-    }
+    if (lane == 63) s_red[wave] = v;
     __syncthreads();
-    int off_a = 0, off_b = 0;
-    total_a = total_b = 0;
+    int off = 0;
+    total = 0;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-        const int xa = s_red[w], xb = s_red[4 + w];
-        off_a += (w < wave) ? xa : 0;
-        off_b += (w < wave) ? xb : 0;
-        total_a += xa;
-        total_b += xb;
+        const int x = s_red[w];
+        off += (w < wave) ? x : 0;
+        total += x;
     }
     __syncthreads();
-    incl_b = b + off_b;
-    return a + off_a;
+    return v + off;
 }
 
 template <typename E, int G, bool PAGED>
@@ -162,7 +153,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // [stage][0 = K, 1 = V][64 keys x 256 B]
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kStages][2][kTileBytes];
     __shared__ int s_red[4 * (kSplitTries + 1)];
-    __shared__ int s_seq, s_ltile, s_item0, s_old;
+    __shared__ int s_seq, s_ltile, s_old;
     __shared__ int s_kend[4];
 
     const int tid = threadIdx.x;
@@ -177,7 +168,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int lin = blockIdx.x;
     int grp, tile_lin;
     int b, tile, q_begin, q_end, kv_len;
-    int piece = 0, npieces = 1, item = 0;  // key split of this query tile
+    // Key split of this query tile: piece `piece` of `npieces`; its siblings
+    // are work items sib_base + p * sib_stride (piece-major order), which
+    // also index their partial slots; the counter is piece 0's.
+    int piece = 0, npieces = 1, sib_base = 0, sib_stride = 0;
     if constexpr (PAGED) {
         const int groups = a.n_kv_heads * a.head_groups;
         bool split = a.part != nullptr;
@@ -276,7 +270,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // along the dispatch order, so no run of long pieces queues behind
         // one shader engine while others idle.
         if (tid == 0) s_seq = -1;
-        int carry = 0, carry_items = 0;
+        int carry = 0;
         for (int base = 0; base < a.num_seqs; base += 256) {
             const int i = base + tid;
             int nt = 0, pp = 1, ql = 0, kvl = 0;
@@ -285,21 +279,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 nt = ql > 0 ? (ql + BT - 1) / BT : 0;
                 pp = split ? pieces_of(kvl, T) : 1;
             }
-            int tot, tot_items;
-            int incl_items;
-            const int incl = block_incl_scan2(nt * pp, nt, s_red, tot, incl_items, tot_items);
+            int tot;
+            const int incl = block_incl_scan(nt * pp, s_red, tot);
             const int excl = incl - nt * pp;
             if (i < a.num_seqs && tile_lin >= carry + excl && tile_lin < carry + incl) {
                 s_seq = i;
                 s_ltile = tile_lin - carry - excl;
-                s_item0 = carry_items + incl_items - nt;
                 s_kend[0] = i < 256 ? my_q0 : a.cu_seqlens[i];  // q_begin (s_kend is rewritten below)
                 s_kend[1] = ql;
                 s_kend[2] = kvl;
                 s_kend[3] = pp;
             }
             carry += tot;
-            carry_items += tot_items;
             if (carry > tile_lin) break;
         }
         __syncthreads();
@@ -311,8 +302,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         npieces = s_kend[3];
         const int nt = (s_kend[1] + BT - 1) / BT;
         piece = s_ltile / nt;
-        tile = nt - 1 - (s_ltile - piece * nt);  // heaviest tile of the sequence first
-        item = grp * a.items_per_group + s_item0 + tile;
+        const int jh = s_ltile - piece * nt;
+        tile = nt - 1 - jh;  // heaviest tile of the sequence first
+        sib_base = w - s_ltile + jh;
+        sib_stride = nt;
         __syncthreads();  // s_kend is reused below
     } else {
         const int per_xcd = (int)gridDim.x >> 3;
@@ -346,12 +339,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int npages_tbl = PAGED ? min(a.num_pages_per_seq, (kv_len + kPage - 1) / kPage) : 0;
     const int lrow = lane >> 4;  // row within the load's group of 4
     const int lpos = lane & 15;
-    int koff[4], voff[4];        // byte offset of this lane's chunk inside its row
+    // Byte offsets of this lane's chunks: inside its row (koff, voff) and
+    // inside a full page of the pool (kfull, vfull, rows 4j + lrow).  The
+    // copies of a full tile use the precomputed page offsets, so the issue
+    // path does no address arithmetic that could tie it to a pending load.
+    const int rs_k = (int)a.k_stride2 * EB, rs_v = (int)a.v_stride2 * EB;
+    int koff[4], voff[4], kfull[4], vfull[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = 4 * j + lrow;
         koff[j] = ((lpos ^ swz_k(r)) << 4);
         voff[j] = ((lpos ^ swz_v(r)) << 4);
+        kfull[j] = r * rs_k + koff[j];
+        vfull[j] = r * rs_v + voff[j];
     }
     // Block ids for this wave's page of tiles tbase .. tbase+63, one per lane.
     int tbl = -1, tbase = 0;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int last_row = kv_len - 1 - (kc & ~15);
         const char* kp;
         const char* vp;
-        int rs_k, rs_v;
+        bool ok = true;
         if constexpr (PAGED) {
             int blk = -1;
             if (key0 < kv_len) {
@@ -379,27 +379,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 blk = pg < npages_tbl ? table[pg] : -1;
                 blk = __builtin_amdgcn_readfirstlane(blk);
             }
-            const bool ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+            ok = blk >= 0 && (int64_t)blk < a.num_blocks;
             kp = ok ? kbase_p + ((int64_t)blk * a.k_stride0 + (int64_t)kvh * a.k_stride1) * EB
                     : reinterpret_cast<const char*>(g_zero_page);
             vp = ok ? vbase_p + ((int64_t)blk * a.v_stride0 + (int64_t)kvh * a.v_stride1) * EB
                     : reinterpret_cast<const char*>(g_zero_page);
-            rs_k = ok ? (int)a.k_stride2 * EB : kRowBytes;
-            rs_v = ok ? (int)a.v_stride2 * EB : kRowBytes;
         } else {
             const int k16 = kc & ~15;
             kp = kbase_p + ((int64_t)b * a.k_stride0 + (int64_t)kvh * a.k_stride1 + (int64_t)k16 * a.k_stride2) * EB;
             vp = vbase_p + ((int64_t)b * a.v_stride0 + (int64_t)kvh * a.v_stride1 + (int64_t)k16 * a.v_stride2) * EB;
-            rs_k = (int)a.k_stride2 * EB;
-            rs_v = (int)a.v_stride2 * EB;
         }
         const uint32_t kd = lds_addr(&smem[stage][0][(16 * wave) * kRowBytes]);
         const uint32_t vd = lds_addr(&smem[stage][1][(16 * wave) * kRowBytes]);
+        if (ok && last_row >= kPage - 1) {  // a full page of the pool (wave-uniform)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = min(4 * j + lrow, last_row);
-            lds_dma16(kp, (uint32_t)(row * rs_k + koff[j]), kd + j * 1024);
-            lds_dma16(vp, (uint32_t)(row * rs_v + voff[j]), vd + j * 1024);
+            for (int j = 0; j < 4; ++j) {
+                lds_dma16(kp, (uint32_t)kfull[j], kd + j * 1024);
+                lds_dma16(vp, (uint32_t)vfull[j], vd + j * 1024);
+            }
+        } else {
+            // The sequence's last page (rows past kv_len repeat its last row)
+            // or the zero page (every row reads row 0: all of it is zeros).
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = ok ? min(4 * j + lrow, last_row) : 0;
+                lds_dma16(kp, (uint32_t)(row * rs_k + koff[j]), kd + j * 1024);
+                lds_dma16(vp, (uint32_t)(row * rs_v + voff[j]), vd + j * 1024);
+            }
         }
     };
 
@@ -592,35 +598,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // Partial of this piece, lane-major so each lane later reads back
         // exactly its own values: accumulator k = 4*dt + g of lane l of wave
         // w at 16 * ((16 w + k) * 64 + l), (m, l) at 65536 + 8 * (64 w + l).
-        uint8_t* slots = reinterpret_cast<uint8_t*>(a.part) + (int64_t)item * kMaxPieces * kPartSlotBytes;
+        // Piece p's slot is its work index sib_base + p * sib_stride (< the
+        // resident workgroup count, as split calls have no more pieces).
+        uint8_t* part = reinterpret_cast<uint8_t*>(a.part);
+        auto slot_of = [&](int p) { return part + (int64_t)(sib_base + p * sib_stride) * kPartSlotBytes; };
+        const int lane_acc = (wave * 16 * 64 + lane) * 16;  // + k * 1024
+        const int lane_ml = 65536 + (wave * 64 + lane) * 8;
         {
-            const auto r = slot_rsrc(slots + (int64_t)piece * kPartSlotBytes);
+            const auto r = slot_rsrc(slot_of(piece));
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    sys_store16(r, ((wave * 16 + 4 * dt + g) * 64 + lane) * 16,
+                    sys_store16(r, lane_acc + (4 * dt + g) * 1024,
                                 f32x4{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]});
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l_run)}, r,
-                                                  65536 + (wave * 64 + lane) * 8, 0, 0x11);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l_run)}, r, lane_ml, 0,
+                                                  0x11);
         }
         // The partial is in memory before the count goes up.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (tid == 0)
-            s_old = __hip_atomic_fetch_add(a.counters + item, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int* counter = a.counters + sib_base;
+        if (tid == 0) s_old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         if (s_old != nne - 1) return;  // another piece merges
-        if (tid == 0) __hip_atomic_exchange(a.counters + item, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("" ::: "memory");
-        for (int q = 0; q < nne; ++q) {
-            if (q == piece) continue;
-            const auto r = slot_rsrc(slots + (int64_t)q * kPartSlotBytes);
-            const auto mlv = __builtin_amdgcn_raw_buffer_load_b64(r, 65536 + (wave * 64 + lane) * 8, 0, 0x11);
-            f32x4 v[16];
+        // Merge the other pieces' partials; the next one's loads are in
+        // flight while the current one is folded in.
+        f32x4 cur[16], nxt[16];
+        u32x2 cml = {0u, 0u}, nml = {0u, 0u};
+        auto load_part = [&](int p, f32x4 (&v)[16], u32x2& ml) {
+            const auto r = slot_rsrc(slot_of(p));
+            ml = __builtin_amdgcn_raw_buffer_load_b64(r, lane_ml, 0, 0x11);
 #pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = sys_load16(r, ((wave * 16 + k) * 64 + lane) * 16);
-            const float m_o = __uint_as_float(mlv[0]), l_o = __uint_as_float(mlv[1]);
+            for (int k = 0; k < 16; ++k) v[k] = sys_load16(r, lane_acc + k * 1024);
+        };
+        int q = piece == 0 ? 1 : 0;
+        load_part(q, cur, cml);
+        while (q < nne) {
+            int qn = q + 1;
+            if (qn == piece) ++qn;
+            if (qn < nne) load_part(qn, nxt, nml);
+            const float m_o = __uint_as_float(cml[0]), l_o = __uint_as_float(cml[1]);
             const float m_new = fmaxf(m_run, m_o);
             const float al = fast_exp2(m_run - m_new), be = fast_exp2(m_o - m_new);
             l_run = l_run * al + l_o * be;
@@ -630,16 +650,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) oacc[dt][4 * g + e] = oacc[dt][4 * g + e] * al + v[4 * dt + g][e] * be;
+                    for (int e = 0; e < 4; ++e) oacc[dt][4 * g + e] = oacc[dt][4 * g + e] * al + cur[4 * dt + g][e] * be;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) cur[k] = nxt[k];
+            cml = nml;
+            q = qn;
         }
         // Every partial was consumed (the merged values depend on them):
         // clear the slots for later calls.
-        for (int q = 0; q < nne; ++q) {
-            uint8_t* sq = slots + (int64_t)q * kPartSlotBytes;
+        for (int p = 0; p < nne; ++p) {
+            uint8_t* sp = slot_of(p);
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                *reinterpret_cast<f32x4*>(sq + ((wave * 16 + k) * 64 + lane) * 16) = f32x4{0.f, 0.f, 0.f, 0.f};
-            *reinterpret_cast<u32x2*>(sq + 65536 + (wave * 64 + lane) * 8) = u32x2{0u, 0u};
+            for (int k = 0; k < 16; ++k) *reinterpret_cast<f32x4*>(sp + lane_acc + k * 1024) = f32x4{0.f, 0.f, 0.f, 0.f};
+            *reinterpret_cast<u32x2*>(sp + lane_ml) = u32x2{0u, 0u};
         }
     }
 
@@ -688,20 +711,32 @@ static hipError_t launch_dtype(int dtype, int G, const PrefillArgs& a, hipStream
 
 // Query tiles per (kv head, head group) are at most num_tokens / BT plus one
 // partial tile per sequence.
+// Query tiles per (kv head, head group) are at most num_tokens / BT plus one
+// partial tile per sequence.
 static int prefill_items_per_group(int num_seqs, int num_tokens, int BT) { return (num_tokens + BT - 1) / BT + num_seqs; }
 
-size_t prefill_work_items(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
-    if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) return 0;
-    const int n_rep = n_heads / n_kv_heads;
-    const int G = pick_group(n_rep);
-    return (size_t)prefill_items_per_group(num_seqs, num_tokens, 32 * (4 / G)) * n_kv_heads * (n_rep / G);
+hipError_t prefill_resident_workgroups(int& resident) {
+    // Two workgroups per CU are resident (LDS and register budget).
+    static int cu_count[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    int& cus = cu_count[dev & 63];
+    if (cus == 0) {
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        if (cus <= 0) cus = 1;
+    }
+    resident = 2 * cus;
+    return hipSuccess;
 }
 
-size_t prefill_counter_bytes(size_t items) { return (items * sizeof(int) + 255) & ~(size_t)255; }
+// A split call has at most `resident` pieces in all: one counter and one
+// partial slot per resident workgroup, whatever the batch.
+size_t prefill_counter_bytes(int resident) { return ((size_t)resident * sizeof(int) + 255) & ~(size_t)255; }
 
-size_t prefill_workspace_bytes(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
-    const size_t items = prefill_work_items(num_seqs, num_tokens, n_heads, n_kv_heads);
-    return items ? prefill_counter_bytes(items) + items * kMaxPieces * kPartSlotBytes : 0;
+size_t prefill_workspace_bytes(int resident) {
+    return resident > 0 ? prefill_counter_bytes(resident) + (size_t)resident * kPartSlotBytes : 0;
 }
 
 hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st) {
@@ -709,22 +744,14 @@ hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStr
     const int BT = 32 * (4 / G);
     a.head_groups = a.n_rep / G;
     a.items_per_group = prefill_items_per_group(a.num_seqs, num_tokens, BT);
-    a.tiles_per_group = a.items_per_group * (a.part ? kMaxPieces : 1);
+    a.tiles_per_group = a.items_per_group;
     a.total_work = a.tiles_per_group * a.n_kv_heads * a.head_groups;
     if (num_tokens <= 0 || a.num_seqs <= 0) return hipSuccess;
     if (a.part) {
-        // Two workgroups per CU are resident (LDS and register budget).
-        static int cu_count[64] = {0};
-        int dev = 0;
-        hipError_t e = hipGetDevice(&dev);
+        hipError_t e = prefill_resident_workgroups(a.resident);
         if (e != hipSuccess) return e;
-        int& cus = cu_count[dev & 63];
-        if (cus == 0) {
-            e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-            if (e != hipSuccess) return e;
-            if (cus <= 0) cus = 1;
-        }
-        a.resident = 2 * cus;
+        // a split call has at most `resident` pieces
+        a.total_work = a.total_work > a.resident ? a.total_work : a.resident;
     }
     return launch_dtype<true>(dtype, G, a, st);
 }

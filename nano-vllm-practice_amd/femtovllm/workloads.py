@@ -248,6 +248,16 @@ def prefill_bf16_long_llama3_8b(poison=True) -> PagedWorkload:
     )
 
 
+def prefill_bf16_long_tp8_share(poison=True) -> PagedWorkload:
+    """One GPU's share of the long-context workload under 8-way tensor parallelism
+    (Llama-3-8B shape split by KV head): 4 query heads and 1 KV head, one
+    32768-token sequence, cut into chunks by ``long_context_chunk``."""
+    return make_paged_workload(
+        "prefill_bf16_llama3_8b_32k_tp8", [(0, 32768)], 4, 1,
+        seed=1004, poison=poison,
+    )
+
+
 def long_context_chunk(w: PagedWorkload, c: int, chunk: int = 2048, device=None, Q_TILE_SIZE=32):
     """Chunk ``c`` of the long-context sequence: ``chunk`` new tokens after a ``chunk*c`` prefix."""
     device = device or w.q.device

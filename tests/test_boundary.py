@@ -95,15 +95,15 @@ def test_gemm_rejects_fp32(C):
 
 
 def test_gemm_workspace_size_and_checks(C):
+    # The size is one slot per resident workgroup of the current device (0
+    # without a device, as here); empty calls and bad head counts need none.
     size = C._lib.femto_paged_attention_gemm_workspace_size
     assert size(0, 16, 16, 8) == 0 and size(2, 0, 16, 8) == 0
-    small, big = size(2, 100, 16, 8), size(8, 4096, 16, 8)
-    assert big > small > 0 and small % 4 == 0
-    assert size(8, 4096, 32, 8) > 0 and size(8, 4096, 12, 8) == 0  # heads not a multiple of kv heads
-    # a workspace that is too small is rejected before launch (bf16, 2 sequences, 10 tokens)
+    assert size(8, 4096, 12, 8) == 0  # heads not a multiple of kv heads
+    # with a workspace the call sizes it against the device: without one it fails cleanly
     rc = C._lib.femto_paged_attention_gemm(2, 16, 128, 128, 16, 128, 128, 16, 16, 8, 8, 16, 128, 16384, 2048, 128,
                                            16, 2, 10, 16, 16, 4, 4, 16, 16, 256, 64, None)
-    assert rc == 1 and "workspace" in C._lib.femto_attn_last_error().decode()
+    assert rc != 0 and C._lib.femto_attn_last_error().decode()
 
 
 def test_flash_validation(C):

@@ -1,0 +1,81 @@
+"""Static check of the prefill kernels' gfx950 code (CPU only: hipcc -S).
+
+Each wave stages its page of the next K/V tile with eight direct-to-LDS copies
+(global_load_lds_dwordx4, issued from inline asm, which the compiler's wait
+counting does not see).  If the compiler puts an ``s_waitcnt vmcnt`` between
+those copies -- it did when a copy offset was built with v_mad_u64_u32 on a
+register pair whose high half held a pending block-table load -- every tile
+waits for its own copies and the kernel loses 10-15 %.  This test compiles
+csrc/paged_prefill.hip with the library's flags and asserts that no basic
+block of any instantiation has such a wait between its copies.
+"""
+
+import importlib.util
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "nano-vllm-practice_amd")
+
+
+def _compile_to_asm(tmp_path):
+    # the library's build script: same hipcc and flags
+    spec = importlib.util.spec_from_file_location("femto_build", os.path.join(PKG, "build.py"))
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+
+    try:
+        hipcc = build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc not available")
+    out = tmp_path / "paged_prefill.s"
+    flags = [f for f in build.HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+    cmd = [hipcc, *flags, "--cuda-device-only", "-S", "-I", build.INCLUDE, "-I", build.CSRC,
+           os.path.join(build.CSRC, "paged_prefill.hip"), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    return out.read_text()
+
+
+def _kernels(asm):
+    lines = asm.split("\n")
+    starts = [(i, l.split(":")[0]) for i, l in enumerate(lines)
+              if re.match(r"^_ZN5femto21attention_mfma_kernel\w+:", l)]
+    for s, name in starts:
+        e = next(j for j in range(s, len(lines)) if lines[j].startswith(".Lfunc_end"))
+        yield name, lines[s:e]
+
+
+def _blocks(body):
+    block, name = [], "entry"
+    for line in body:
+        m = re.match(r"^(\.LBB[\w_]+):", line)
+        if m:
+            yield name, block
+            block, name = [], m.group(1)
+            continue
+        t = line.strip()
+        if t and not t.startswith((";", ".")):
+            block.append(t)
+    yield name, block
+
+
+def test_no_wait_between_tile_copies(tmp_path):
+    asm = _compile_to_asm(tmp_path)
+    kernels = list(_kernels(asm))
+    assert len(kernels) == 12  # {bf16, f16} x G {1, 2, 4} x {paged, dense}
+    bad, blocks_with_copies = [], 0
+    for name, body in kernels:
+        for bname, ins in _blocks(body):
+            copies = [k for k, t in enumerate(ins) if t.startswith("global_load_lds_dwordx4")]
+            if len(copies) < 2:
+                continue
+            blocks_with_copies += 1
+            waits = [t for t in ins[copies[0]:copies[-1]] if t.startswith("s_waitcnt") and "vmcnt" in t]
+            if waits:
+                bad.append((name, bname, waits))
+    assert blocks_with_copies >= 12
+    assert not bad, f"vmcnt waits between direct-to-LDS copies: {bad[:4]}"

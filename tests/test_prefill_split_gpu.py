@@ -2,7 +2,7 @@
 
 With a workspace, femto_paged_attention_gemm cuts the query tiles of
 sequences much longer than the average work per resident workgroup into up
-to four pieces over their keys; the last piece to finish merges the others'
+to eight pieces over their keys; the last piece to finish merges the others'
 partial softmax states within the launch.  The results must match the oracle
 (the reference's attention, paged_attention_gemm.py:83-160) and the unsplit
 kernel, and every call must leave the workspace zero-filled.
@@ -47,7 +47,7 @@ def _workspace_is_zero(device):
 def split_plan(chunks, n_heads, n_kv_heads, cus):
     """Pieces per query tile of each sequence, by the kernel's rule: T = the
     causal-estimated key tiles per resident workgroup (two per CU), pieces =
-    round(key tiles / T) capped at 4; while the pieces do not all fit in the
+    round(key tiles / T) capped at 8; while the pieces do not all fit in the
     resident slots at once, T grows by half (three times at most), then the
     call is not split."""
     n_rep = n_heads // n_kv_heads
@@ -63,7 +63,7 @@ def split_plan(chunks, n_heads, n_kv_heads, cus):
             est += -(-n // BT) * -(-mean_keys // 64)
     T = max(8, -(-est * groups // resident))
     for _ in range(4):
-        pieces = [min(4, max(1, (2 * -(-(p + n) // 64) + T) // (2 * T))) if p + n > 0 else 1 for p, n in chunks]
+        pieces = [min(8, max(1, (2 * -(-(p + n) // 64) + T) // (2 * T))) if p + n > 0 else 1 for p, n in chunks]
         if groups * sum(-(-n // BT) * pp for (p, n), pp in zip(chunks, pieces)) <= resident:
             return pieces
         T += T // 2
@@ -92,8 +92,8 @@ def _check(ops, w, gpu, monkeypatch, rows_per_seq=6, what=""):
 
 
 # One long sequence among short ones: the long one's query tiles are split
-# into 4, 3 or 2 pieces.
-@pytest.mark.parametrize("long_prefix,pieces", [(6000, 4), (1300, 3), (800, 2)])
+# into 8, 6, 3 or 2 pieces.
+@pytest.mark.parametrize("long_prefix,pieces", [(6000, 8), (2600, 6), (1300, 3), (800, 2)])
 def test_long_sequence_among_short(ops, gpu, monkeypatch, long_prefix, pieces):
     chunks = [(long_prefix, 192)] + [(int(p), 64) for p in np.linspace(0, 300, 40)]
     assert split_plan(chunks, 16, 8, _cus())[0] == pieces
@@ -146,7 +146,7 @@ def test_arbitrary_positions_with_split(ops, gpu, monkeypatch):
     """Positions that are not the last q_len keys: some pieces see no visible
     key for some rows (their state is empty and must merge away)."""
     chunks = [(4000, 96), (10, 64), (30, 64), (50, 64)]
-    assert split_plan(chunks, 16, 8, _cus())[0] == 4
+    assert split_plan(chunks, 16, 8, _cus())[0] == 8
     w = workloads.make_paged_workload("splitpos", chunks, 16, 8, seed=91)
     q, meta = w.gemm_call(device=gpu)
     rng = np.random.default_rng(92)
@@ -205,6 +205,40 @@ def test_many_sequences_with_one_split(ops, gpu, monkeypatch):
     (index 300) is split and lives in the second chunk of the kernel's
     per-sequence passes."""
     chunks = [(int(p), 1) for p in np.linspace(10, 500, 300)] + [(8000, 128)]
-    assert split_plan(chunks, 2, 1, _cus())[-1] == 4
+    assert split_plan(chunks, 2, 1, _cus())[-1] == 8
     w = workloads.make_paged_workload("many_split", chunks, 2, 1, seed=261)
     _check(ops, w, gpu, monkeypatch, rows_per_seq=2, what="300 decode + 1 long")
+
+
+def test_tp8_share_long_chunk(ops, gpu, monkeypatch):
+    """One GPU's share under 8-way tensor parallelism (4 query heads, 1 KV
+    head): a 2048-token chunk after a 6144-token prefix has 64 query tiles for
+    the whole GPU, and each is split into 8 pieces."""
+    chunks = [(6144, 2048)]
+    assert split_plan(chunks, 4, 1, _cus()) == [8]
+    w = workloads.make_paged_workload("tp8", chunks, 4, 1, seed=1004)
+    _check(ops, w, gpu, monkeypatch, rows_per_seq=64, what="tp8 share chunk")
+
+
+def test_too_small_workspace_is_rejected(ops, gpu):
+    """The C ABI checks the workspace against one slot per resident workgroup."""
+    from femtovllm import _C
+
+    need = _C._lib.femto_paged_attention_gemm_workspace_size(2, 10, 16, 8)
+    assert need >= _cus() * 2 * 67584
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    q = torch.zeros((16, 10, 128), dtype=torch.bfloat16, device=gpu)
+    pool = torch.zeros((8, 8, 16, 128), dtype=torch.bfloat16, device=gpu)
+    out = torch.empty_like(q)
+    cu = torch.tensor([0, 5, 10], dtype=torch.int32, device=gpu)
+    tables = torch.zeros((2, 4), dtype=torch.int32, device=gpu)
+    kv = torch.tensor([5, 5], dtype=torch.int32, device=gpu)
+    pos = torch.arange(10, dtype=torch.int32, device=gpu) % 5
+    args = [2, q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+            pool.data_ptr(), pool.data_ptr(), 8, 8, 16, 128, pool.stride(0), pool.stride(1), pool.stride(2),
+            cu.data_ptr(), 2, 10, 16, tables.data_ptr(), 4, tables.stride(0), kv.data_ptr(), pos.data_ptr()]
+    rc = _C._lib.femto_paged_attention_gemm(*args, ws.data_ptr(), need - 256, None)
+    assert rc == 1 and "workspace" in _C._lib.femto_attn_last_error().decode()
+    rc = _C._lib.femto_paged_attention_gemm(*args, ws.data_ptr(), need, None)
+    torch.cuda.synchronize()
+    assert rc == 0 and int(torch.count_nonzero(ws)) == 0
