@@ -104,9 +104,11 @@ int femto_paged_attention_gemm(
     void* workspace, size_t workspace_bytes,
     void* stream);
 
-/* Bytes of the optional key-split workspace of femto_paged_attention_gemm
- * (0 for an empty call).  No counterpart in the reference, whose prefill
- * kernels take no workspace. */
+/* Bytes of the optional key-split workspace of femto_paged_attention_gemm:
+ * one counter and one 66 KiB partial slot per workgroup the current device
+ * holds at once (2 per CU), independent of the batch; 0 for an empty call or
+ * without a device.  No counterpart in the reference, whose prefill kernels
+ * take no workspace. */
 size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads);
 
 /* KV-cache write: scatter new K/V rows into the paged pools, bit-exact.
