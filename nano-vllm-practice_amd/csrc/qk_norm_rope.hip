@@ -19,7 +19,10 @@
 // token has H q rows, KVH k rows and KVH v rows of head_dim = 128; a DPP row
 // of 16 lanes handles one of them, lane c holding dims 8c .. 8c + 7, so the
 // sum of squares is a 16-lane DPP reduction and the RoPE partner of dim d
-// (d +- 64) sits in lane c +- 8 (one DPP row rotation).
+// (d +- 64) sits in lane c +- 8 (one DPP row rotation).  Each DPP row loads
+// eight rows at once, and the tokens' cos / sin rows are staged in LDS once
+// per workgroup, so a workgroup waits for about two memory round trips
+// instead of a few per row.
 #include "common.h"
 #include "launch.h"
 
@@ -46,16 +49,38 @@ __device__ __forceinline__ void store8(F32, char* p, const float f[8]) {
     st16(p + 16, u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])});
 }
 
-// Raw copy of 8 elements (v rows).
-__device__ __forceinline__ void copy8(int eb, const char* src, char* dst) {
-    st16(dst, ld16(src));
-    if (eb == 4) st16(dst + 16, ld16(src + 16));
+// Raw 16-byte chunks of one row slice (two for f32: 8 floats).
+template <typename E>
+struct RowRaw {
+    u32x4 w[E::kBytes == 4 ? 2 : 1];
+};
+
+template <typename E>
+__device__ __forceinline__ void load_raw(const char* p, RowRaw<E>& r) {
+    r.w[0] = ld16(p);
+    if constexpr (E::kBytes == 4) r.w[1] = ld16(p + 16);
+}
+template <typename E>
+__device__ __forceinline__ void store_raw(char* p, const RowRaw<E>& r) {
+    st16(p, r.w[0]);
+    if constexpr (E::kBytes == 4) st16(p + 16, r.w[1]);
+}
+__device__ __forceinline__ void raw_to_float(BF16, const RowRaw<BF16>& r, float f[8]) { unpack8(BF16{}, r.w[0], f); }
+__device__ __forceinline__ void raw_to_float(F16, const RowRaw<F16>& r, float f[8]) { unpack8(F16{}, r.w[0], f); }
+__device__ __forceinline__ void raw_to_float(F32, const RowRaw<F32>& r, float f[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i] = __uint_as_float(r.w[0][i]);
+        f[4 + i] = __uint_as_float(r.w[1][i]);
+    }
 }
 
 template <typename E>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     constexpr int EB = E::kBytes;
+    constexpr int kBatch = 8;  // rows in flight per DPP row
     __shared__ int s_stop, s_blk[2];
+    __shared__ float s_rope[kProTokens][2][kDimHead];  // cos, sin rows of the workgroup's tokens
     const int b = blockIdx.y;
     int q_begin, q_end;
     if (a.cw.cu_seqlens) {
@@ -68,97 +93,132 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int t0 = q_begin + (int)blockIdx.x * kProTokens;
     if (t0 >= q_end) return;
     const int t1 = min(q_end, t0 + kProTokens);
+    const int ntok = t1 - t0;
+    const int tid = threadIdx.x;
+
+    // This thread's share of the tokens' cos / sin rows: token tid / 64,
+    // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.  The position load goes
+    // out first; the destination pages are looked up meanwhile.
+    const int rt = tid >> 6, rsel = (tid >> 5) & 1, rd = 4 * (tid & 31);
+    const int pr = rt < ntok ? a.positions_rope[t0 + rt] : -1;
 
     // Destination pages of this workgroup's tokens (as kv_cache_write_kernel).
     const int p0 = a.cw.positions[q_begin];
     const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
     const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
-    if (threadIdx.x == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
+    if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
     __syncthreads();
     if (p0 >= 0) {
         const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
-        for (int c = p0 / kPage + (int)threadIdx.x; c <= colB; c += 256) {
+        for (int c = p0 / kPage + tid; c <= colB; c += 256) {
             const int blk = c < a.cw.num_pages_per_seq ? table[c] : -1;
             if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, c);
             if (c == colA) s_blk[0] = blk;
             if (c == colB) s_blk[1] = blk;
         }
     }
-    __syncthreads();
-    const int stop = s_stop;
 
-    const int lrow = threadIdx.x >> 4;  // DPP row of the workgroup: one (token, head row) at a time
-    const int c = threadIdx.x & 15;     // dims 8c .. 8c + 7
+    const int lrow = tid >> 4;  // DPP row of the workgroup: one (token, head row) at a time
+    const int c = tid & 15;     // dims 8c .. 8c + 7
     const int d0 = 8 * c;
-    float wq[8], wk[8];
-    load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
-    load8(E{}, static_cast<const char*>(a.k_weight) + d0 * EB, wk);
-
     const int H = a.n_heads, KVH = a.cw.n_kv_heads;
     const int R = H + 2 * KVH;  // rows per token: q heads, k heads, v heads
-    const int pairs = (t1 - t0) * R;
-    for (int pi = lrow; pi < pairs; pi += 16) {  // uniform within the DPP row
+    const int pairs = ntok * R;
+
+    // Source of row pi (token t0 + pi / R): q head, k head or v head.
+    auto src_of = [&](int pi) -> const char* {
         const int ti = pi / R;
         const int r = pi - ti * R;
         const int t = t0 + ti;
-        const int pc = p0 + (t - q_begin);  // cache position
-        const int col = pc / kPage;
-        const bool write_cache = p0 >= 0 && col < stop;
-        char* dst = nullptr;
-        if (r >= H && write_cache) {
-            const int h = r < H + KVH ? r - H : r - H - KVH;
-            const int blk = s_blk[col == colA ? 0 : 1];
-            const int64_t el = (int64_t)blk * a.cw.pool_stride_block + (int64_t)h * a.cw.pool_stride_head +
-                               (int64_t)(pc % kPage) * a.cw.pool_stride_row + d0;
-            dst = static_cast<char*>(r < H + KVH ? a.cw.k_pool : a.cw.v_pool) + el * EB;
+        if (r < H)
+            return static_cast<const char*>(a.q) + ((int64_t)t * a.q_stride_token + (int64_t)r * a.q_stride_head + d0) * EB;
+        if (r < H + KVH)
+            return static_cast<const char*>(a.cw.k) +
+                   ((int64_t)t * a.cw.k_stride_token + (int64_t)(r - H) * a.cw.k_stride_head + d0) * EB;
+        return static_cast<const char*>(a.cw.v) +
+               ((int64_t)t * a.cw.v_stride_token + (int64_t)(r - H - KVH) * a.cw.v_stride_head + d0) * EB;
+    };
+
+    // First batch of rows: loads in flight with the rope rows and the pages.
+    RowRaw<E> raw[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+        const int pi = lrow + 16 * k;
+        if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
+    }
+    {
+        float4 v4;
+        if (pr >= 0 && pr < a.rope_rows) {
+            const float* tab = rsel ? a.sin : a.cos;
+            v4 = *reinterpret_cast<const float4*>(tab + (int64_t)pr * a.rope_stride + rd);
+        } else {  // a position outside the tables: NaN rows
+            v4 = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
         }
-        if (r >= H + KVH) {  // v: plain copy
-            if (dst) {
-                const int h = r - H - KVH;
-                const char* src = static_cast<const char*>(a.cw.v) +
-                                  ((int64_t)t * a.cw.v_stride_token + (int64_t)h * a.cw.v_stride_head + d0) * EB;
-                copy8(EB, src, dst);
+        if (rt < ntok) *reinterpret_cast<float4*>(&s_rope[rt][rsel][rd]) = v4;
+    }
+    float wq[8], wk[8];
+    load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
+    load8(E{}, static_cast<const char*>(a.k_weight) + d0 * EB, wk);
+    __syncthreads();
+    const int stop = s_stop;
+
+    for (int base = 0; base < pairs; base += 16 * kBatch) {
+        if (base > 0) {
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int pi = base + lrow + 16 * k;
+                if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
             }
-            continue;
         }
-        const bool is_q = r < H;
-        const int h = is_q ? r : r - H;
-        const char* src = is_q ? static_cast<const char*>(a.q) + ((int64_t)t * a.q_stride_token + (int64_t)h * a.q_stride_head + d0) * EB
-                               : static_cast<const char*>(a.cw.k) + ((int64_t)t * a.cw.k_stride_token + (int64_t)h * a.cw.k_stride_head + d0) * EB;
-        float x[8];
-        load8(E{}, src, x);
-        // RMSNorm over the 128 dims of the row.
-        float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-        ss = row16_sum(ss);
-        const float rinv = 1.0f / sqrtf(ss * (1.0f / kDimHead) + a.eps);
-        const float* w = is_q ? wq : wk;
+        for (int k = 0; k < kBatch; ++k) {
+            const int pi = base + lrow + 16 * k;  // uniform within the DPP row
+            if (pi >= pairs) break;
+            const int ti = pi / R;
+            const int r = pi - ti * R;
+            const int t = t0 + ti;
+            const int pc = p0 + (t - q_begin);  // cache position
+            const int col = pc / kPage;
+            const bool write_cache = p0 >= 0 && col < stop;
+            char* dst = nullptr;
+            if (r >= H && write_cache) {
+                const int h = r < H + KVH ? r - H : r - H - KVH;
+                const int blk = s_blk[col == colA ? 0 : 1];
+                const int64_t el = (int64_t)blk * a.cw.pool_stride_block + (int64_t)h * a.cw.pool_stride_head +
+                                   (int64_t)(pc % kPage) * a.cw.pool_stride_row + d0;
+                dst = static_cast<char*>(r < H + KVH ? a.cw.k_pool : a.cw.v_pool) + el * EB;
+            }
+            if (r >= H + KVH) {  // v: plain copy
+                if (dst) store_raw<E>(dst, raw[k]);
+                continue;
+            }
+            const bool is_q = r < H;
+            float x[8];
+            raw_to_float(E{}, raw[k], x);
+            // RMSNorm over the 128 dims of the row.
+            float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = x[i] * rinv * w[i];
-        // RoPE at this token's position: rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] above.
-        const int pr = a.positions_rope[t];
-        const bool in_table = pr >= 0 && pr < a.rope_rows;
-        float cs[8], sn[8];
-        if (in_table) {
-            load8(F32{}, reinterpret_cast<const char*>(a.cos + (int64_t)pr * a.rope_stride + d0), cs);
-            load8(F32{}, reinterpret_cast<const char*>(a.sin + (int64_t)pr * a.rope_stride + d0), sn);
-        } else {
+            for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+            ss = row16_sum(ss);
+            const float rinv = 1.0f / sqrtf(ss * (1.0f / kDimHead) + a.eps);
+            const float* w = is_q ? wq : wk;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) cs[i] = sn[i] = __builtin_nanf("");
-        }
-        float o[8];
+            for (int i = 0; i < 8; ++i) x[i] = x[i] * rinv * w[i];
+            // RoPE at this token's position: rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] above.
+            float o[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float partner = dpp_f32<0x128>(x[i]);  // lane c +- 8 (row_ror:8)
-            const float rot = c < 8 ? -partner : partner;
-            o[i] = fmaf(cs[i], x[i], sn[i] * rot);
-        }
-        if (is_q) {
-            char* qo = static_cast<char*>(a.q_out) + ((int64_t)t * a.q_out_stride_token + (int64_t)h * a.q_out_stride_head + d0) * EB;
-            store8(E{}, qo, o);
-        } else if (dst) {
-            store8(E{}, dst, o);
+            for (int i = 0; i < 8; ++i) {
+                const float partner = dpp_f32<0x128>(x[i]);  // lane c +- 8 (row_ror:8)
+                const float rot = c < 8 ? -partner : partner;
+                o[i] = fmaf(s_rope[ti][0][d0 + i], x[i], s_rope[ti][1][d0 + i] * rot);
+            }
+            if (is_q) {
+                char* qo = static_cast<char*>(a.q_out) +
+                           ((int64_t)t * a.q_out_stride_token + (int64_t)r * a.q_out_stride_head + d0) * EB;
+                store8(E{}, qo, o);
+            } else if (dst) {
+                store8(E{}, dst, o);
+            }
         }
     }
 }
