@@ -33,7 +33,7 @@
 //    range of KV heads, keeping a head's pages in one L2;
 //  * key split (paged, when the caller gives a workspace): a query tile
 //    whose sequence is much longer than the average work per resident
-//    workgroup is cut into P <= 4 pieces over its key tiles, so one long
+//    workgroup is cut into P <= 8 pieces over its key tiles, so one long
 //    sequence no longer sets the length of the whole call; only when all
 //    pieces fit in the resident workgroup slots at once.  Every piece
 //    writes its partial (m, l, O) with system-scope stores (written through
@@ -57,8 +57,9 @@ constexpr int kTileBytes = kKvTile * kRowBytes;        // 16 KB per K or V tile
 constexpr float kEmptyMaxP = -1.0e30f;
 constexpr int kSplitTries = 4;  // key-split granularities tried (T grows by half each time)
 
-// One page of zeros: the source of every load whose block id lies outside
-// the pool, so such a page reads as zeros without a branch.
+// One page of zeros: the source of every copy whose block id lies outside
+// the pool (each of its rows is read from row 0), so such a page reads as
+// zeros.
 __device__ __attribute__((aligned(16))) uint16_t g_zero_page[kPage * kDimHead];
 
 // 16-byte chunk c of LDS row r lives at chunk position c ^ swz(r).
@@ -175,10 +176,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (PAGED) {
         const int groups = a.n_kv_heads * a.head_groups;
         bool split = a.part != nullptr;
-        // Pieces per query tile of sequence i: round(key tiles / T), where T
-        // is the estimated key tiles per resident workgroup of the whole call
-        // (query tile j of a chunk of ql tokens sees about kv_len - ql + BT (j+1)
-        // keys).  A sequence no longer than the average is never split.
         // Per-sequence sizes, loaded once: thread t keeps sequence t (the
         // passes below reload only for sequences past the first 256).
         int my_q0 = 0, my_ql = 0, my_kvl = 0;
@@ -196,7 +193,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 kvl = a.kv_lens[i];
             }
         };
-        // T: causal-estimated key tiles per resident workgroup of the call.
+        // Pieces per query tile of sequence i: round(key tiles / T), at most
+        // kMaxPieces, where T0 is the estimated key tiles per resident
+        // workgroup of the whole call (query tile j of a chunk of ql tokens
+        // sees about kv_len - ql + BT (j+1) keys).  A sequence up to 1.5 times
+        // the average is not split.
         int T0 = 0;
         if (split) {
             for (int base = 0; base < a.num_seqs; base += 256) {
