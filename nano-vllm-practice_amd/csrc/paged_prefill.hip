@@ -740,8 +740,6 @@ static hipError_t launch_dtype(int dtype, int G, const PrefillArgs& a, hipStream
 
 // Query tiles per (kv head, head group) are at most num_tokens / BT plus one
 // partial tile per sequence.
-// Query tiles per (kv head, head group) are at most num_tokens / BT plus one
-// partial tile per sequence.
 static int prefill_items_per_group(int num_seqs, int num_tokens, int BT) { return (num_tokens + BT - 1) / BT + num_seqs; }
 
 hipError_t prefill_resident_workgroups(int& resident) {
