@@ -46,6 +46,28 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f32<0x128>(x));
+    x = fmaxf(x, dpp_f32<0x124>(x));
+    x = fmaxf(x, dpp_f32<0x4E>(x));
+    x = fmaxf(x, dpp_f32<0xB1>(x));
+    return x;
+}
+
+// Wave total / maximum, in every lane: the four row results (lanes 0, 16,
+// 32, 48) combined through scalar reads.
+__device__ __forceinline__ float lane_f32(float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+__device__ __forceinline__ float wave_sum_f32(float x) {
+    x = row16_sum(x);
+    return (lane_f32(x, 0) + lane_f32(x, 16)) + (lane_f32(x, 32) + lane_f32(x, 48));
+}
+__device__ __forceinline__ float wave_max_f32(float x) {
+    x = row16_max(x);
+    return fmaxf(fmaxf(lane_f32(x, 0), lane_f32(x, 16)), fmaxf(lane_f32(x, 32), lane_f32(x, 48)));
+}
+
 __device__ __forceinline__ float shfl_xor_f32(float x, int mask) { return __shfl_xor(x, mask, kWave); }
 
 // ---- element types -----------------------------------------------------

@@ -404,18 +404,14 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
     // slot's weight exp2(m_i - M) goes to LDS.
     const float mi = t < count ? m_ld : kEmptyMax;
     const float li = t < count ? l_ld : 0.0f;
-    float M = mi;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, shfl_xor_f32(M, off));
+    float M = wave_max_f32(mi);
     __shared__ float s_m[2];
     if ((t & 63) == 0) s_m[t >> 6] = M;
     __syncthreads();
     M = fmaxf(s_m[0], s_m[1]);
     const float wi = t < count ? fast_exp2(mi - M) : 0.0f;
     s_w[t] = wi;
-    float lw = li * wi;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) lw += shfl_xor_f32(lw, off);
+    const float lw = wave_sum_f32(li * wi);
     __shared__ float s_ls[2];
     if ((t & 63) == 0) s_ls[t >> 6] = lw;
     __syncthreads();
