@@ -70,6 +70,21 @@ __device__ __forceinline__ float wave_max_f32(float x) {
 
 __device__ __forceinline__ float shfl_xor_f32(float x, int mask) { return __shfl_xor(x, mask, kWave); }
 
+// Row pairs through v_permlane16_swap / v_permlane32_swap (VALU, no LDS):
+// a = x of the first row of each pair (rows 0 and 2 for 16; lanes 0-31 for
+// 32) and b = x of the second (rows 1 and 3; lanes 32-63), in every lane of
+// the pair.
+__device__ __forceinline__ void pair16(float x, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float x, float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    a = __uint_as_float(r[0]);
+    b = __uint_as_float(r[1]);
+}
+
 // ---- element types -----------------------------------------------------
 struct BF16 {
     using mfma_vec = bf16x8;

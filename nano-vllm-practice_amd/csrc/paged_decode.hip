@@ -327,25 +327,30 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
             }
         }
 
-        // Merge the four DPP rows (same dims, different keys).
+        // Merge the four DPP rows (same dims, different keys): rows 0+1 and
+        // 2+3, then the two halves; every lane of a pair ends with the pair's
+        // state (the first row's terms first, as row 0 computes them).
+        auto merge_pair = [&](auto pair) {
 #pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-#pragma unroll
-            for (int sh = 16; sh <= 32; sh *= 2) {
-                const float mo = shfl_xor_f32(m[r], sh);
-                const float lo = shfl_xor_f32(l[r], sh);
-                const float mn = fmaxf(m[r], mo);
-                const float fa = fast_exp2(m[r] - mn);
-                const float fb = fast_exp2(mo - mn);
-                l[r] = l[r] * fa + lo * fb;
+            for (int r = 0; r < NREP; ++r) {
+                float m0, m1, l0, l1;
+                pair(m[r], m0, m1);
+                pair(l[r], l0, l1);
+                const float mn = fmaxf(m0, m1);
+                const float f0 = fast_exp2(m0 - mn);
+                const float f1 = fast_exp2(m1 - mn);
+                l[r] = l0 * f0 + l1 * f1;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float ao = shfl_xor_f32(acc[r][e], sh);
-                    acc[r][e] = acc[r][e] * fa + ao * fb;
+                    float a0, a1;
+                    pair(acc[r][e], a0, a1);
+                    acc[r][e] = a0 * f0 + a1 * f1;
                 }
                 m[r] = mn;
             }
-        }
+        };
+        merge_pair([](float x, float& a, float& b) { pair16(x, a, b); });
+        merge_pair([](float x, float& a, float& b) { pair32(x, a, b); });
 
         // Partial state of this segment.
         const int slot = wi - S / C;
