@@ -127,6 +127,24 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
            __builtin_amdgcn_readlane(v, 48);
 }
 
+// Wave minimum / maximum, to every lane.
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, dpp_i32<0x128>(v));
+    v = max(v, dpp_i32<0x124>(v));
+    v = max(v, dpp_i32<0x4E>(v));
+    v = max(v, dpp_i32<0xB1>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, dpp_i32<0x128>(v));
+    v = min(v, dpp_i32<0x124>(v));
+    v = min(v, dpp_i32<0x4E>(v));
+    v = min(v, dpp_i32<0xB1>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 // Inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 inside each row,
 // then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then
 // the total of rows 0-1 into rows 2-3 (row_bcast:31).
@@ -462,17 +480,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     } else {
         lim = kv_len;
     }
-    int kend_w = qvalid ? lim : 0;
-    int kfull_w = qvalid ? lim : 0x7fffffff;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        kend_w = max(kend_w, __shfl_xor(kend_w, o, 64));
-        kfull_w = min(kfull_w, __shfl_xor(kfull_w, o, 64));
-    }
-    // Both are wave-uniform after the reductions; say so, so that the tile
-    // loop branches on scalars.
-    kend_w = __builtin_amdgcn_readfirstlane(kend_w);
-    kfull_w = __builtin_amdgcn_readfirstlane(kfull_w);
+    // Wave-uniform (scalar) limits, so that the tile loop branches on scalars.
+    const int kend_w = wave_max_i32(qvalid ? lim : 0);
+    const int kfull_w = wave_min_i32(qvalid ? lim : 0x7fffffff);
     if (lane == 0) s_kend[wave] = kend_w;
     __syncthreads();
     const int kend = max(max(s_kend[0], s_kend[1]), max(s_kend[2], s_kend[3]));
@@ -560,7 +570,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[kb2][i]);
             }
         }
-        mx = fmaxf(mx, shfl_xor_f32(mx, 32)) * scale;
+        {
+            float m_lo, m_hi;  // the row's two lane halves (keys 4*h2 + ...)
+            pair32(mx, m_lo, m_hi);
+            mx = fmaxf(m_lo, m_hi) * scale;
+        }
         // Lazy rescale: the running max m_run only moves when some row's
         // max exceeds it by more than 8 (log2 units), so exponentials stay
         // <= 2^8 and O is rarely rescaled.
@@ -697,7 +711,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // ---- epilogue: O^T accumulator i of dim tile dt holds dim
     // 32*dt + 8*(i/4) + 4*h2 + i%4 of this lane's query.
-    const float l_tot = l_run + shfl_xor_f32(l_run, 32);
+    float l_lo, l_hi;
+    pair32(l_run, l_lo, l_hi);
+    const float l_tot = l_lo + l_hi;
     const float inv_l = 1.0f / l_tot;  // 0 visible keys: 1/0 = inf, and 0 * inf = NaN as in the reference
     if (qvalid) {
         char* orow = reinterpret_cast<char*>(a.out) +
