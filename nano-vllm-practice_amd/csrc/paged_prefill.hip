@@ -78,7 +78,11 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // straight into LDS at lds_base + 16 * lane.  Issued through asm so the
 // compiler does not order later LDS reads of the other stage behind it; the
 // kernel waits for these copies itself (vmcnt) before the stage is read.
-// base and lds_base must be the same in every lane of the wave.
+// base and lds_base must be the same in every lane of the wave.  m0 is on the
+// clobber list; clang warns that it is reserved, but nothing else in these
+// kernels uses m0 (their assembly sets it only here), so the warning is muted.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds_base) {
     const uint64_t b = (uint64_t)(uintptr_t)base;
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
@@ -92,6 +96,7 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint3
         : "v"(voff), "s"(sb), "s"(m0v)
         : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
