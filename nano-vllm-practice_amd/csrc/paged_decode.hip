@@ -6,22 +6,24 @@
 // key j of sequence b at k_pool[tables[b][j / 16], h / n_rep, j % 16].
 //
 // Design (memory-bound GEMV):
-//  * one workgroup = (split of the sequence's pages, KV head, head group of
-//    NREP query heads); every K/V byte is loaded once and used by all NREP
-//    query heads that share the KV head (the reference loads it n_rep times);
-//  * 4 waves take the split's pages round-robin; inside a wave, DPP row r
-//    (16 lanes) owns page rows r, r+4, r+8, r+12 and lane c of the row owns 8
-//    head dims, so each K/V page is 4 coalesced 16-byte loads per lane
-//    (bf16/f16; f32 uses 8) and the q.k reduction stays inside a DPP row;
+//  * waves are independent workers: per group of NREP query heads sharing a
+//    KV head, the pages of all sequences are concatenated and cut into equal
+//    slices, one per wave (one wave per SIMD); every K/V byte is loaded once
+//    and used by all NREP query heads (the reference loads it n_rep times);
+//  * inside a wave, DPP row r (16 lanes) owns page rows r, r+4, r+8, r+12 and
+//    lane c of the row owns 8 head dims, so each K/V page is 4 coalesced
+//    16-byte loads per lane (bf16/f16; f32 uses 8), issued with the
+//    non-temporal hint (each byte is read once per call), and the q.k
+//    reduction stays inside a DPP row;
 //  * block ids are fetched 64 at a time (one per lane) and broadcast with
 //    readlane, and each wave keeps two pages of loads in flight, so the
 //    table never adds a dependent load per page;
 //  * every lane keeps an online-softmax state (max, sum, 8 accumulators) per
-//    query head over the keys it saw; states merge across DPP rows with
-//    shuffles and across waves through LDS; split sequences leave one
-//    partial state per split in the workspace and a small merge kernel on
-//    the same stream combines them (no cross-workgroup fences or atomics,
-//    which on gfx950 would write back and invalidate the XCD's L2);
+//    query head over the keys it saw; states merge across the four DPP rows
+//    with permlane swaps, each sequence segment of a slice leaves one partial
+//    state in the workspace, and a small merge kernel on the same stream
+//    combines them (no cross-workgroup fences or atomics, which on gfx950
+//    would write back and invalidate the XCD's L2);
 //  * rows past kv_len are never read (loads are clamped to the last visible
 //    row and their scores masked) and block ids outside the pool are never
 //    dereferenced (their page reads as zeros), so NaN in unused pool memory
@@ -39,6 +41,7 @@ template <>
 struct RowSlice<BF16> {
     u32x4 w;
     __device__ __forceinline__ void load(const char* row, int c) { w = ld16(row + 16 * c); }
+    __device__ __forceinline__ void stream(const char* row, int c) { w = ld16_nt(row + 16 * c); }
     __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
     __device__ __forceinline__ void to_float(float f[8]) const { unpack8(BF16{}, w, f); }
     static __device__ __forceinline__ int dim(int c, int e) { return 8 * c + e; }
@@ -48,6 +51,7 @@ template <>
 struct RowSlice<F16> {
     u32x4 w;
     __device__ __forceinline__ void load(const char* row, int c) { w = ld16(row + 16 * c); }
+    __device__ __forceinline__ void stream(const char* row, int c) { w = ld16_nt(row + 16 * c); }
     __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
     __device__ __forceinline__ void to_float(float f[8]) const { unpack8(F16{}, w, f); }
     static __device__ __forceinline__ int dim(int c, int e) { return 8 * c + e; }
@@ -61,6 +65,10 @@ struct RowSlice<F32> {
     __device__ __forceinline__ void load(const char* row, int c) {
         a = ld16(row + 16 * c);
         b = ld16(row + 256 + 16 * c);
+    }
+    __device__ __forceinline__ void stream(const char* row, int c) {
+        a = ld16_nt(row + 16 * c);
+        b = ld16_nt(row + 256 + 16 * c);
     }
     __device__ __forceinline__ void zero() {
         a = u32x4{0, 0, 0, 0};
@@ -101,27 +109,6 @@ struct PageRegs {
     RowSlice<E> k[4], v[4];
 };
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
-__device__ __forceinline__ int wave_max(int v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, kWave));
-    return v;
-}
-
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(v, o, kWave);
-        if (lane >= o) v += u;
-    }
-    return v;
-}
-
 __device__ __forceinline__ int pages_of(int kv_len) { return kv_len > 0 ? (kv_len + kPage - 1) / kPage : 0; }
 
 // Load-balanced split-KV decode.  Every wave is an independent worker: the
@@ -153,8 +140,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         total += pg;
         longest = max(longest, pg);
     }
-    total = wave_sum(total);
-    longest = wave_max(longest);
+    total = wave_sum_i32(total);
+    longest = wave_max_i32(longest);
     int C = (total + a.waves_per_group - 1) / a.waves_per_group;
     C = max(C, a.min_chunk_pages);
     C = max(C, (longest + a.max_slots - 2) / (a.max_slots - 1));  // at most max_slots slots per sequence
@@ -170,9 +157,9 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
         const int i = base + lane;
         my_len = i < B ? a.kv_lens[i] : 0;
         const int pg = pages_of(my_len);
-        const int incl = wave_incl_scan(pg, lane);
+        const int incl = wave_incl_scan_i32(pg);
         my_excl = carry + incl - pg;
-        chunk_total = __shfl(incl, kWave - 1, kWave);
+        chunk_total = __builtin_amdgcn_readlane(incl, kWave - 1);
         if (x0 < carry + chunk_total) break;
         carry += chunk_total;
     }
@@ -196,12 +183,12 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
             const int i = base + lane;
             my_len = i < B ? a.kv_lens[i] : 0;
             const int pg = pages_of(my_len);
-            const int incl = wave_incl_scan(pg, lane);
+            const int incl = wave_incl_scan_i32(pg);
             my_excl = carry + incl - pg;
-            chunk_total = __shfl(incl, kWave - 1, kWave);
+            chunk_total = __builtin_amdgcn_readlane(incl, kWave - 1);
         }
-        const int kv_len = __shfl(my_len, b - base, kWave);
-        const int S = __shfl(my_excl, b - base, kWave);
+        const int kv_len = __builtin_amdgcn_readlane(my_len, b - base);  // b - base is wave-uniform
+        const int S = __builtin_amdgcn_readlane(my_excl, b - base);
         const int npg = pages_of(kv_len);
         if (npg == 0 || S + npg <= x) {
             ++b;
@@ -246,8 +233,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
             for (int j = 0; j < 4; ++j) {
                 const int row = min(rg + 4 * j, last_row);
                 const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
-                pr.k[j].load(kpool + off, c);
-                pr.v[j].load(vpool + off, c);
+                pr.k[j].stream(kpool + off, c);
+                pr.v[j].stream(vpool + off, c);
             }
         };
         auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {

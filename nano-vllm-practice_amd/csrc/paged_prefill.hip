@@ -115,54 +115,6 @@ __device__ __forceinline__ f32x4 sys_load16(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0x11));
 }
 
-// DPP on 32-bit ints: rows (16 lanes) enabled by kRowMask; a lane whose
-// source lies outside its row, or whose row is disabled, gets 0.
-template <int kCtrl, int kRowMask = 0xf>
-__device__ __forceinline__ int dpp_i32(int x) {
-    return __builtin_amdgcn_update_dpp(0, x, kCtrl, kRowMask, 0xf, false);
-}
-
-// Wave sum, to every lane: DPP inside each 16-lane row, then the four rows.
-__device__ __forceinline__ int wave_sum_i32(int v) {
-    v += dpp_i32<0x128>(v);  // row_ror:8
-    v += dpp_i32<0x124>(v);  // row_ror:4
-    v += dpp_i32<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_i32<0xB1>(v);   // quad_perm [1,0,3,2]
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
-           __builtin_amdgcn_readlane(v, 48);
-}
-
-// Wave minimum / maximum, to every lane.
-__device__ __forceinline__ int wave_max_i32(int v) {
-    v = max(v, dpp_i32<0x128>(v));
-    v = max(v, dpp_i32<0x124>(v));
-    v = max(v, dpp_i32<0x4E>(v));
-    v = max(v, dpp_i32<0xB1>(v));
-    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-__device__ __forceinline__ int wave_min_i32(int v) {
-    v = min(v, dpp_i32<0x128>(v));
-    v = min(v, dpp_i32<0x124>(v));
-    v = min(v, dpp_i32<0x4E>(v));
-    v = min(v, dpp_i32<0xB1>(v));
-    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
-}
-
-// Inclusive scan over the 64 lanes: row_shr 1, 2, 4, 8 inside each row,
-// then row 0's total into row 1 and row 2's into row 3 (row_bcast:15), then
-// the total of rows 0-1 into rows 2-3 (row_bcast:31).
-__device__ __forceinline__ int wave_incl_scan_i32(int x) {
-    x += dpp_i32<0x111>(x);
-    x += dpp_i32<0x112>(x);
-    x += dpp_i32<0x114>(x);
-    x += dpp_i32<0x118>(x);
-    x += dpp_i32<0x142, 0xa>(x);
-    x += dpp_i32<0x143, 0xc>(x);
-    return x;
-}
-
 // Sums of N values over the workgroup (every thread gets them); s_red holds 4 * N ints.
 template <int N>
 __device__ __forceinline__ void block_reduce_n(int (&v)[N], int* s_red) {
