@@ -596,23 +596,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     if (PAGED && nne > 1) {
         // Partial of this piece, lane-major so each lane later reads back
-        // exactly its own values: accumulator k = 4*dt + g of lane l of wave
-        // w at 16 * ((16 w + k) * 64 + l), (m, l) at 65536 + 8 * (64 w + l).
+        // exactly its own values.  f32 and f16 storage: the raw accumulators,
+        // accumulator k = 4*dt + g of lane l of wave w at
+        // 16 * ((16 w + k) * 64 + l), and (m, l) per lane.  bf16 storage:
+        // the accumulators divided by the row sum and by a power of two
+        // 2^e above their largest magnitude, as fp16 (8 per 16 bytes, chunk
+        // k = 2*dt + j at 16 * ((8 w + k) * 64 + l); 2^e as f32 at
+        // 32768 + 4 * (64 w + l)), and (m, row sum): half the bytes, which
+        // is what a merge costs (one CU reads the other pieces' partials at
+        // ~23 GB/s), for an added error of at most 2^-12 of the lane's
+        // largest output, below the bf16 output rounding.  (m, l) at
+        // 65536 + 8 * (64 w + l) in both layouts.
         // Piece p's slot is its work index sib_base + p * sib_stride (< the
         // resident workgroup count, as split calls have no more pieces).
+        constexpr bool kHalf = std::is_same<E, BF16>::value;
         uint8_t* part = reinterpret_cast<uint8_t*>(a.part);
         auto slot_of = [&](int p) { return part + (int64_t)(sib_base + p * sib_stride) * kPartSlotBytes; };
-        const int lane_acc = (wave * 16 * 64 + lane) * 16;  // + k * 1024
+        const int lane_acc = (wave * (kHalf ? 8 : 16) * 64 + lane) * 16;  // + k * 1024
         const int lane_ml = 65536 + (wave * 64 + lane) * 8;
         {
             const auto r = slot_rsrc(slot_of(piece));
+            float l_pub = l_run;
+            if constexpr (kHalf) {
+                float l_lo, l_hi;
+                pair32(l_run, l_lo, l_hi);
+                l_pub = l_lo + l_hi;
+                float amax = 0.0f;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+                for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    sys_store16(r, lane_acc + (4 * dt + g) * 1024,
-                                f32x4{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]});
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l_run)}, r, lane_ml, 0,
+                    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(oacc[dt][e]));
+                const float inv = l_pub > 0.0f ? 1.0f / l_pub : 0.0f;
+                int ex = 0;
+                frexpf(amax * inv, &ex);  // amax * inv < 2^ex
+                const float sc = ldexpf(inv, -ex), unsc = ldexpf(1.0f, ex);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        float f[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) f[e] = oacc[dt][8 * j + e] * sc;
+                        __builtin_amdgcn_raw_buffer_store_b128(pack8(F16{}, f), r, lane_acc + (2 * dt + j) * 1024, 0,
+                                                               0x11);
+                    }
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(unsc), r, 32768 + (wave * 64 + lane) * 4, 0, 0x11);
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        sys_store16(r, lane_acc + (4 * dt + g) * 1024,
+                                    f32x4{oacc[dt][4 * g], oacc[dt][4 * g + 1], oacc[dt][4 * g + 2], oacc[dt][4 * g + 3]});
+            }
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l_pub)}, r, lane_ml, 0,
                                                   0x11);
         }
         // The partial is in memory before the count goes up.
@@ -624,44 +661,95 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (s_old != nne - 1) return;  // another piece merges
         if (tid == 0) __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("" ::: "memory");
-        // Merge the other pieces' partials; the next one's loads are in
-        // flight while the current one is folded in.
-        f32x4 cur[16], nxt[16];
-        u32x2 cml = {0u, 0u}, nml = {0u, 0u};
-        auto load_part = [&](int p, f32x4 (&v)[16], u32x2& ml) {
-            const auto r = slot_rsrc(slot_of(p));
-            ml = __builtin_amdgcn_raw_buffer_load_b64(r, lane_ml, 0, 0x11);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = sys_load16(r, lane_acc + k * 1024);
+        // Merge the other pieces' partials, kR per round with all their
+        // loads in flight together.  The piece indices are made scalar so
+        // the slots' buffer descriptors are scalar (no per-lane descriptor
+        // loop around each load), and each round is straight-line code, so
+        // it waits for its own loads only.  A round with fewer partials
+        // reads its last one again and gives the copies weight 0.
+        constexpr int kR = kHalf ? 4 : 2;
+        constexpr int kLoads = kHalf ? 8 : 16;
+        const int pc = __builtin_amdgcn_readfirstlane(piece);
+        const int n_o = __builtin_amdgcn_readfirstlane(nne) - 1;
+        const int sb = __builtin_amdgcn_readfirstlane(sib_base);
+        const int ss = __builtin_amdgcn_readfirstlane(sib_stride);
+        auto other_rsrc = [&](int i) {  // the i-th other piece, this one skipped
+            return slot_rsrc(part + (int64_t)(sb + (i < pc ? i : i + 1) * ss) * kPartSlotBytes);
         };
-        int q = piece == 0 ? 1 : 0;
-        load_part(q, cur, cml);
-        while (q < nne) {
-            int qn = q + 1;
-            if (qn == piece) ++qn;
-            if (qn < nne) load_part(qn, nxt, nml);
-            const float m_o = __uint_as_float(cml[0]), l_o = __uint_as_float(cml[1]);
-            const float m_new = fmaxf(m_run, m_o);
-            const float al = fast_exp2(m_run - m_new), be = fast_exp2(m_o - m_new);
-            l_run = l_run * al + l_o * be;
+#pragma unroll 1
+        for (int i = 0; i < n_o; i += kR) {
+            __amdgpu_buffer_rsrc_t r[kR];
+            u32x2 ml[kR];
+            uint32_t sc[kR];
+            u32x4 v[kR][kLoads];
+#pragma unroll
+            for (int j = 0; j < kR; ++j) {
+                r[j] = other_rsrc(min(i + j, n_o - 1));
+                ml[j] = __builtin_amdgcn_raw_buffer_load_b64(r[j], lane_ml, 0, 0x11);
+                if constexpr (kHalf) sc[j] = __builtin_amdgcn_raw_buffer_load_b32(r[j], 32768 + (wave * 64 + lane) * 4, 0, 0x11);
+            }
+#pragma unroll
+            for (int j = 0; j < kR; ++j)
+#pragma unroll
+                for (int k = 0; k < kLoads; ++k)
+                    v[j][k] = __builtin_amdgcn_raw_buffer_load_b128(r[j], lane_acc + k * 1024, 0, 0x11);
+            float m_new = m_run;
+#pragma unroll
+            for (int j = 0; j < kR; ++j) m_new = fmaxf(m_new, __uint_as_float(ml[j][0]));
+            const float al = fast_exp2(m_run - m_new);
+            float w[kR], wsum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kR; ++j) {
+                w[j] = i + j < n_o ? fast_exp2(__uint_as_float(ml[j][0]) - m_new) : 0.0f;
+                if constexpr (kHalf) w[j] *= __uint_as_float(ml[j][1]);  // fp16 partials are normalised
+                else wsum += w[j] * __uint_as_float(ml[j][1]);
+            }
+            if constexpr (kHalf) {
+#pragma unroll
+                for (int j = 0; j < kR; ++j) {
+                    wsum += w[j];
+                    w[j] *= __uint_as_float(sc[j]);  // undo the partial's power-of-two scale
+                }
+                // Each half-wave keeps half of the merged pieces' row sum, so
+                // the two halves still add up to the row total.
+                l_run = l_run * al + 0.5f * wsum;
+            } else {
+                l_run = l_run * al + wsum;
+            }
             m_run = m_new;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-                for (int g = 0; g < 4; ++g)
+                for (int e = 0; e < 16; ++e) oacc[dt][e] *= al;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) oacc[dt][4 * g + e] = oacc[dt][4 * g + e] * al + cur[4 * dt + g][e] * be;
+            for (int j = 0; j < kR; ++j) {
 #pragma unroll
-            for (int k = 0; k < 16; ++k) cur[k] = nxt[k];
-            cml = nml;
-            q = qn;
+                for (int dt = 0; dt < 4; ++dt) {
+                    if constexpr (kHalf) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            float f[8];
+                            unpack8(F16{}, v[j][2 * dt + h], f);
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) oacc[dt][8 * h + e] = fmaf(f[e], w[j], oacc[dt][8 * h + e]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int g = 0; g < 4; ++g)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                oacc[dt][4 * g + e] = fmaf(__uint_as_float(v[j][4 * dt + g][e]), w[j], oacc[dt][4 * g + e]);
+                    }
+                }
+            }
         }
         // Every partial was consumed (the merged values depend on them):
         // clear the slots for later calls.
         for (int p = 0; p < nne; ++p) {
             uint8_t* sp = slot_of(p);
 #pragma unroll
-            for (int k = 0; k < 16; ++k) *reinterpret_cast<f32x4*>(sp + lane_acc + k * 1024) = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < kLoads; ++k) *reinterpret_cast<f32x4*>(sp + lane_acc + k * 1024) = f32x4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (kHalf) *reinterpret_cast<uint32_t*>(sp + 32768 + (wave * 64 + lane) * 4) = 0u;
             *reinterpret_cast<u32x2*>(sp + lane_ml) = u32x2{0u, 0u};
         }
     }

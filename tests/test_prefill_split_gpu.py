@@ -8,6 +8,8 @@ partial softmax states within the launch.  The results must match the oracle
 kernel, and every call must leave the workspace zero-filled.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -218,6 +220,30 @@ def test_tp8_share_long_chunk(ops, gpu, monkeypatch):
     assert split_plan(chunks, 4, 1, _cus()) == [8]
     w = workloads.make_paged_workload("tp8", chunks, 4, 1, seed=1004)
     _check(ops, w, gpu, monkeypatch, rows_per_seq=64, what="tp8 share chunk")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_split_values_beyond_fp16_range(ops, gpu, monkeypatch, dtype):
+    """bf16 key-split partials travel as fp16 scaled by a per-lane power of
+    two.  V scaled by 2^18 (past fp16's 65504, exact in bf16) must give the
+    output scaled by 2^18, split and unsplit (f16 storage keeps fp32
+    partials and is checked the same way at 2^10)."""
+    chunks = [(6000, 192)] + [(int(p), 64) for p in np.linspace(0, 300, 40)]
+    assert split_plan(chunks, 16, 8, _cus())[0] == 8
+    w = workloads.make_paged_workload("split_range", chunks, 16, 8, dtype=dtype, seed=81, poison=False)
+    scale = 2.0**18 if dtype == torch.bfloat16 else 2.0**10
+    q, meta = w.gemm_call(device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    big = dataclasses.replace(wd, v_pool=wd.v_pool * scale)
+    assert torch.isfinite(big.v_pool).all()
+    out = _gemm(ops, q, meta, wd)
+    out_big = _gemm(ops, q, meta, big)
+    assert torch.isfinite(out_big).all()
+    assert_close(out_big.float() / scale, out.float().cpu().numpy(), dtype, "V x 2^k, split")
+    ref_big = _unsplit(ops, q, meta, big, monkeypatch)
+    assert_close(out_big.float() / scale, (ref_big.float() / scale).cpu().numpy(), dtype, "V x 2^k vs unsplit")
+    assert _workspace_is_zero(gpu)
 
 
 def test_too_small_workspace_is_rejected(ops, gpu):
