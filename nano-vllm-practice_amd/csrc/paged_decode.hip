@@ -16,7 +16,7 @@
 //    non-temporal hint (each byte is read once per call), and the q.k
 //    reduction stays inside a DPP row;
 //  * block ids are fetched 64 at a time (one per lane) and broadcast with
-//    readlane, and each wave keeps two pages of loads in flight, so the
+//    readlane, and each wave keeps three pages of loads in flight, so the
 //    table never adds a dependent load per page;
 //  * every lane keeps an online-softmax state (max, sum, 8 accumulators) per
 //    query head over the keys it saw; states merge across the four DPP rows
@@ -294,23 +294,32 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
             }
         };
 
-        // Two pages in flight: page i+1 loads while page i computes.
-        PageRegs<E> ra, rb;
-        bool ok_a = false, ok_b = false;
+        // Three pages in flight: pages i+1 and i+2 load while page i
+        // computes (96 KB of loads per CU at one wave per SIMD).
+        PageRegs<E> r0, r1, r2;
+        bool k0 = false, k1 = false, k2 = false;
         fetch_table(0);
-        issue(0, ra, ok_a);
-        for (int i = 0; i < n; i += 2) {
-            if (i + 1 < n) {
-                if (((i + 1) & 63) == 0) fetch_table(i + 1);
-                issue(i + 1, rb, ok_b);
+        issue(0, r0, k0);
+        if (1 < n) issue(1, r1, k1);
+        for (int i = 0; i < n; i += 3) {
+            if (i + 2 < n) {
+                if (((i + 2) & 63) == 0) fetch_table(i + 2);
+                issue(i + 2, r2, k2);
             }
-            consume(i, ra, ok_a);
+            consume(i, r0, k0);
             if (i + 1 < n) {
-                if (i + 2 < n) {
-                    if (((i + 2) & 63) == 0) fetch_table(i + 2);
-                    issue(i + 2, ra, ok_a);
+                if (i + 3 < n) {
+                    if (((i + 3) & 63) == 0) fetch_table(i + 3);
+                    issue(i + 3, r0, k0);
                 }
-                consume(i + 1, rb, ok_b);
+                consume(i + 1, r1, k1);
+                if (i + 2 < n) {
+                    if (i + 4 < n) {
+                        if (((i + 4) & 63) == 0) fetch_table(i + 4);
+                        issue(i + 4, r1, k1);
+                    }
+                    consume(i + 2, r2, k2);
+                }
             }
         }
 
