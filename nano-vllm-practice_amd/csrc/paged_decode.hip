@@ -427,10 +427,12 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
 
 template <typename E, int NREP>
 static hipError_t launch_t(DecodeArgs a, int num_seqs, hipStream_t st) {
-    // One wave per SIMD (4 per CU), each with two pages of K and V in flight
-    // (64 KB per CU).  HBM read throughput peaks there: more resident waves
-    // queue more requests and lose bandwidth (on the 545 MB Qwen3-0.6B-shaped
-    // batch, 16 waves per CU ran at 4.85 TB/s and 4 per CU at 5.2 TB/s).
+    // One wave per SIMD (4 per CU), each with three pages of K and V in
+    // flight (96 KB per CU).  HBM read throughput peaks there: more resident
+    // waves queue more requests and lose bandwidth (on the 545 MB
+    // Qwen3-0.6B-shaped batch, 16 waves per CU ran at 4.85 TB/s and 4 per CU
+    // at 5.2 TB/s with ordinary loads; 8 per CU with non-temporal loads was
+    // 2 % slower than 4).
     static int cu_count[64] = {0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
