@@ -373,8 +373,8 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 // per head dim.  Runs after the split kernel on the same stream.
 template <typename E>
 __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
-    __shared__ float s_w[128];
-    __shared__ float s_l;
+    __shared__ float s_w[128];  // slot maxima
+    __shared__ float s_lv[128];  // slot sums
     const int h = blockIdx.x;
     const int b = blockIdx.y;
     const int t = threadIdx.x;
@@ -401,28 +401,29 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
         return;
     }
     const int count = count_ld;
-    // thread i < count holds slot i's (m, l); wave-reduce the max, then every
-    // slot's weight exp2(m_i - M) goes to LDS.
-    const float mi = t < count ? m_ld : kEmptyMax;
-    const float li = t < count ? l_ld : 0.0f;
-    float M = wave_max_f32(mi);
-    __shared__ float s_m[2];
-    if ((t & 63) == 0) s_m[t >> 6] = M;
+    // Thread i < count publishes slot i's (m, l); after one barrier every
+    // thread folds the count slots itself (a sequence spans a few slices,
+    // at most max_slots <= 128), so no further reduction round is needed.
+    if (t < count) {
+        s_w[t] = m_ld;
+        s_lv[t] = l_ld;
+    }
     __syncthreads();
-    M = fmaxf(s_m[0], s_m[1]);
-    const float wi = t < count ? fast_exp2(mi - M) : 0.0f;
-    s_w[t] = wi;
-    const float lw = wave_sum_f32(li * wi);
-    __shared__ float s_ls[2];
-    if ((t & 63) == 0) s_ls[t >> 6] = lw;
-    __syncthreads();
-    if (t == 0) s_l = s_ls[0] + s_ls[1];
-    __syncthreads();
-    float O = 0.0f;
+    float M = kEmptyMax;
+    for (int i = 0; i < count; ++i) M = fmaxf(M, s_w[i]);
+    float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kSpec; ++i) O = fmaf(i < count ? v[i] : 0.0f, s_w[i], O);
-    for (int i = kSpec; i < count; ++i) O = fmaf(src[(int64_t)i * kDimHead], s_w[i], O);
-    store_elem<E>(out, o, O / s_l);
+    for (int i = 0; i < kSpec; ++i) {
+        const float wi = i < count ? fast_exp2(s_w[i < count ? i : 0] - M) : 0.0f;
+        L = fmaf(i < count ? s_lv[i] : 0.0f, wi, L);
+        O = fmaf(i < count ? v[i] : 0.0f, wi, O);
+    }
+    for (int i = kSpec; i < count; ++i) {
+        const float wi = fast_exp2(s_w[i] - M);
+        L = fmaf(s_lv[i], wi, L);
+        O = fmaf(src[(int64_t)i * kDimHead], wi, O);
+    }
+    store_elem<E>(out, o, O / L);
 }
 
 template <typename E, int NREP>
