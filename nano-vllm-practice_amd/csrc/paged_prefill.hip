@@ -838,8 +838,18 @@ hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStr
     if (a.part) {
         hipError_t e = prefill_resident_workgroups(a.resident);
         if (e != hipSuccess) return e;
-        // a split call has at most `resident` pieces
-        a.total_work = a.total_work > a.resident ? a.total_work : a.resident;
+        // A split needs all pieces in the resident slots at once, and a call
+        // has at least ceil(num_tokens / BT) query tiles per KV head group:
+        // when those already fill the slots the call cannot split, and the
+        // kernel skips its split estimate.
+        const int64_t min_tiles = (int64_t)((num_tokens + BT - 1) / BT) * a.n_kv_heads * a.head_groups;
+        if (min_tiles >= a.resident) {
+            a.part = nullptr;
+            a.counters = nullptr;
+        } else {
+            // a split call has at most `resident` pieces
+            a.total_work = a.total_work > a.resident ? a.total_work : a.resident;
+        }
     }
     return launch_dtype<true>(dtype, G, a, st);
 }
