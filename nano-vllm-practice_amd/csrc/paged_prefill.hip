@@ -225,77 +225,101 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // candidates T0, 1.5 T0, 2.25 T0, 3.375 T0 (fewer sequences split
         // each time) the first whose pieces all fit in the resident slots at
         // once is taken, else the call runs unsplit.
-        int Tk[kSplitTries];
-        Tk[0] = T0;
-#pragma unroll
-        for (int k = 1; k < kSplitTries; ++k) Tk[k] = Tk[k - 1] + Tk[k - 1] / 2;
-        auto pieces_of = [&](int kvl, int t) {
-            const int ub = kvl > 0 ? (kvl + kKvTile - 1) / kKvTile : 0;
-            return min(kMaxPieces, max(1, (2 * ub + t) / (2 * t)));
-        };
-        int cnt[kSplitTries + 1] = {};  // pieces per KV head group for each T; last: unsplit
-        for (int base = 0; base < a.num_seqs; base += 256) {
-            const int i = base + tid;
-            int c[kSplitTries + 1] = {};
-            if (i < a.num_seqs) {
-                int ql, kvl;
-                seq_sizes(i, ql, kvl);
-                const int nt = ql > 0 ? (ql + BT - 1) / BT : 0;
-#pragma unroll
-                for (int k = 0; k < kSplitTries; ++k) c[k] = split ? nt * pieces_of(kvl, Tk[k]) : nt;
-                c[kSplitTries] = nt;
+        int w = 0;
+        if (tid == 0) s_seq = -1;
+        if (!split && a.num_seqs <= 256) {
+            // Unsplit call, one sequence per thread: a single scan gives both
+            // the work total and each sequence's first query tile.
+            const int nt = tid < a.num_seqs && my_ql > 0 ? (my_ql + BT - 1) / BT : 0;
+            int total;
+            const int incl = block_incl_scan(nt, s_red, total);
+            const int work = groups * total;
+            const int per_xcd = (work + 7) >> 3;
+            if ((lin >> 3) >= per_xcd) return;
+            w = (lin & 7) * per_xcd + (lin >> 3);
+            if (w >= work) return;
+            grp = w / total;
+            tile_lin = w - grp * total;
+            if (nt > 0 && tile_lin >= incl - nt && tile_lin < incl) {
+                s_seq = tid;
+                s_ltile = tile_lin - (incl - nt);
+                s_kend[0] = my_q0;  // q_begin (s_kend is rewritten below)
+                s_kend[1] = my_ql;
+                s_kend[2] = my_kvl;
+                s_kend[3] = 1;
             }
-            block_reduce_n(c, s_red);
+        } else {
+            int Tk[kSplitTries];
+            Tk[0] = T0;
 #pragma unroll
-            for (int k = 0; k <= kSplitTries; ++k) cnt[k] += c[k];
-        }
-        int T = 0, total = cnt[kSplitTries];
-        if (split) {
+            for (int k = 1; k < kSplitTries; ++k) Tk[k] = Tk[k - 1] + Tk[k - 1] / 2;
+            auto pieces_of = [&](int kvl, int t) {
+                const int ub = kvl > 0 ? (kvl + kKvTile - 1) / kKvTile : 0;
+                return min(kMaxPieces, max(1, (2 * ub + t) / (2 * t)));
+            };
+            int cnt[kSplitTries + 1] = {};  // pieces per KV head group for each T; last: unsplit
+            for (int base = 0; base < a.num_seqs; base += 256) {
+                const int i = base + tid;
+                int c[kSplitTries + 1] = {};
+                if (i < a.num_seqs) {
+                    int ql, kvl;
+                    seq_sizes(i, ql, kvl);
+                    const int nt = ql > 0 ? (ql + BT - 1) / BT : 0;
 #pragma unroll
-            for (int k = kSplitTries - 1; k >= 0; --k) {
-                if ((int64_t)groups * cnt[k] <= a.resident) {
-                    T = Tk[k];
-                    total = cnt[k];
+                    for (int k = 0; k < kSplitTries; ++k) c[k] = split ? nt * pieces_of(kvl, Tk[k]) : nt;
+                    c[kSplitTries] = nt;
+                }
+                block_reduce_n(c, s_red);
+#pragma unroll
+                for (int k = 0; k <= kSplitTries; ++k) cnt[k] += c[k];
+            }
+            int T = 0, total = cnt[kSplitTries];
+            if (split) {
+#pragma unroll
+                for (int k = kSplitTries - 1; k >= 0; --k) {
+                    if ((int64_t)groups * cnt[k] <= a.resident) {
+                        T = Tk[k];
+                        total = cnt[k];
+                    }
                 }
             }
-        }
-        split = T > 0;
-        const int work = groups * total;
-        const int per_xcd = (work + 7) >> 3;
-        if ((lin >> 3) >= per_xcd) return;
-        const int w = (lin & 7) * per_xcd + (lin >> 3);
-        if (w >= work) return;
-        grp = w / total;
-        tile_lin = w - grp * total;
+            split = T > 0;
+            const int work = groups * total;
+            const int per_xcd = (work + 7) >> 3;
+            if ((lin >> 3) >= per_xcd) return;
+            w = (lin & 7) * per_xcd + (lin >> 3);
+            if (w >= work) return;
+            grp = w / total;
+            tile_lin = w - grp * total;
 
-        // The sequence of piece tile_lin.  Within a sequence come first the
-        // first pieces of all its query tiles (heaviest, i.e. last, tile
-        // first), then the second pieces, and so on: lengths fall smoothly
-        // along the dispatch order, so no run of long pieces queues behind
-        // one shader engine while others idle.
-        if (tid == 0) s_seq = -1;
-        int carry = 0;
-        for (int base = 0; base < a.num_seqs; base += 256) {
-            const int i = base + tid;
-            int nt = 0, pp = 1, ql = 0, kvl = 0;
-            if (i < a.num_seqs) {
-                seq_sizes(i, ql, kvl);
-                nt = ql > 0 ? (ql + BT - 1) / BT : 0;
-                pp = split ? pieces_of(kvl, T) : 1;
+            // The sequence of piece tile_lin.  Within a sequence come first the
+            // first pieces of all its query tiles (heaviest, i.e. last, tile
+            // first), then the second pieces, and so on: lengths fall smoothly
+            // along the dispatch order, so no run of long pieces queues behind
+            // one shader engine while others idle.
+            int carry = 0;
+            for (int base = 0; base < a.num_seqs; base += 256) {
+                const int i = base + tid;
+                int nt = 0, pp = 1, ql = 0, kvl = 0;
+                if (i < a.num_seqs) {
+                    seq_sizes(i, ql, kvl);
+                    nt = ql > 0 ? (ql + BT - 1) / BT : 0;
+                    pp = split ? pieces_of(kvl, T) : 1;
+                }
+                int tot;
+                const int incl = block_incl_scan(nt * pp, s_red, tot);
+                const int excl = incl - nt * pp;
+                if (i < a.num_seqs && tile_lin >= carry + excl && tile_lin < carry + incl) {
+                    s_seq = i;
+                    s_ltile = tile_lin - carry - excl;
+                    s_kend[0] = i < 256 ? my_q0 : a.cu_seqlens[i];  // q_begin (s_kend is rewritten below)
+                    s_kend[1] = ql;
+                    s_kend[2] = kvl;
+                    s_kend[3] = pp;
+                }
+                carry += tot;
+                if (carry > tile_lin) break;
             }
-            int tot;
-            const int incl = block_incl_scan(nt * pp, s_red, tot);
-            const int excl = incl - nt * pp;
-            if (i < a.num_seqs && tile_lin >= carry + excl && tile_lin < carry + incl) {
-                s_seq = i;
-                s_ltile = tile_lin - carry - excl;
-                s_kend[0] = i < 256 ? my_q0 : a.cu_seqlens[i];  // q_begin (s_kend is rewritten below)
-                s_kend[1] = ql;
-                s_kend[2] = kvl;
-                s_kend[3] = pp;
-            }
-            carry += tot;
-            if (carry > tile_lin) break;
         }
         __syncthreads();
         b = s_seq;
