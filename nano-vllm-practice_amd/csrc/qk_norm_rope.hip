@@ -15,20 +15,23 @@
 // caller's fp32 tables (rope_rows, head_dim); a position outside them gives
 // NaN rows, where the reference's index would raise.
 //
-// Work: workgroup (x, b) takes tokens q_begin + 4x .. + 3 of sequence b.  A
-// token has H q rows, KVH k rows and KVH v rows of head_dim = 128; a DPP row
-// of 16 lanes handles one of them, lane c holding dims 8c .. 8c + 7, so the
-// sum of squares is a 16-lane DPP reduction and the RoPE partner of dim d
-// (d +- 64) sits in lane c +- 8 (one DPP row rotation).  Each DPP row loads
-// eight rows at once, and the tokens' cos / sin rows are staged in LDS once
-// per workgroup, so a workgroup waits for about two memory round trips
-// instead of a few per row.
+// Work: workgroup (x, b) takes tokens q_begin + 4x .. + 3 of sequence b.
+// A token has H q rows, KVH k rows and KVH v rows of head_dim = 128; a DPP
+// row of 16 lanes handles one of them, lane c holding dims 8c .. 8c + 7, so
+// the sum of squares is a 16-lane DPP reduction and the RoPE partner of dim
+// d (d +- 64) sits in lane c +- 8 (one DPP row rotation).  Rows move in
+// batches of eight per DPP row (128 per workgroup), two batches in flight:
+// the first two are loaded before the position and block-table lookups
+// (which take two dependent round trips), and each register buffer is
+// refilled as soon as its batch is stored.  The tokens' cos / sin rows are
+// staged in LDS once per workgroup.
 #include "common.h"
 #include "launch.h"
 
 namespace femto {
 
-constexpr int kProTokens = 4;  // tokens per workgroup
+constexpr int kProTokens = 4;  // tokens per workgroup (a multiple of 4; at most 16, which touch at most two pages)
+constexpr int kProBatch = 8;    // rows per DPP row in one batch (128 rows per workgroup)
 
 // 8 elements at p (16 bytes for 16-bit types, 32 bytes for f32) as floats.
 __device__ __forceinline__ void load8(BF16, const char* p, float f[8]) { unpack8(BF16{}, ld16(p), f); }
@@ -78,7 +81,6 @@ __device__ __forceinline__ void raw_to_float(F32, const RowRaw<F32>& r, float f[
 template <typename E>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     constexpr int EB = E::kBytes;
-    constexpr int kBatch = 8;  // rows in flight per DPP row
     __shared__ int s_stop, s_blk[2];
     __shared__ float s_rope[kProTokens][2][kDimHead];  // cos, sin rows of the workgroup's tokens
     const int b = blockIdx.y;
@@ -95,28 +97,6 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int t1 = min(q_end, t0 + kProTokens);
     const int ntok = t1 - t0;
     const int tid = threadIdx.x;
-
-    // This thread's share of the tokens' cos / sin rows: token tid / 64,
-    // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.  The position load goes
-    // out first; the destination pages are looked up meanwhile.
-    const int rt = tid >> 6, rsel = (tid >> 5) & 1, rd = 4 * (tid & 31);
-    const int pr = rt < ntok ? a.positions_rope[t0 + rt] : -1;
-
-    // Destination pages of this workgroup's tokens (as kv_cache_write_kernel).
-    const int p0 = a.cw.positions[q_begin];
-    const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
-    const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
-    if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
-    __syncthreads();
-    if (p0 >= 0) {
-        const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
-        for (int c = p0 / kPage + tid; c <= colB; c += 256) {
-            const int blk = c < a.cw.num_pages_per_seq ? table[c] : -1;
-            if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, c);
-            if (c == colA) s_blk[0] = blk;
-            if (c == colB) s_blk[1] = blk;
-        }
-    }
 
     const int lrow = tid >> 4;  // DPP row of the workgroup: one (token, head row) at a time
     const int c = tid & 15;     // dims 8c .. 8c + 7
@@ -138,23 +118,55 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
         return static_cast<const char*>(a.cw.v) +
                ((int64_t)t * a.cw.v_stride_token + (int64_t)(r - H - KVH) * a.cw.v_stride_head + d0) * EB;
     };
-
-    // First batch of rows: loads in flight with the rope rows and the pages.
-    RowRaw<E> raw[kBatch];
+    // A batch is kProBatch rows per DPP row (128 rows per workgroup).
+    auto load_batch = [&](int base, RowRaw<E>(&raw)[kProBatch]) {
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-        const int pi = lrow + 16 * k;
-        if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
+        for (int k = 0; k < kProBatch; ++k) {
+            const int pi = base + lrow + 16 * k;
+            if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
+        }
+    };
+
+    // The first two batches of rows depend only on cu_seqlens: their loads
+    // go out before anything else, so the position and block-table lookups
+    // below wait while the rows are already on their way.
+    RowRaw<E> ra[kProBatch], rb[kProBatch];
+    load_batch(0, ra);
+    if (pairs > 16 * kProBatch) load_batch(16 * kProBatch, rb);
+
+    // This thread's share of the tokens' cos / sin rows: tokens tid / 64 + 4i,
+    // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.
+    const int rt = tid >> 6, rsel = (tid >> 5) & 1, rd = 4 * (tid & 31);
+    int pr[kProTokens / 4];
+#pragma unroll
+    for (int i = 0; i < kProTokens / 4; ++i) pr[i] = rt + 4 * i < ntok ? a.positions_rope[t0 + rt + 4 * i] : -1;
+
+    // Destination pages of this workgroup's tokens (as kv_cache_write_kernel;
+    // they touch at most two pages).
+    const int p0 = a.cw.positions[q_begin];
+    const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
+    const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
+    if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
+    __syncthreads();
+    if (p0 >= 0) {
+        const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
+        for (int tc = p0 / kPage + tid; tc <= colB; tc += 256) {
+            const int blk = tc < a.cw.num_pages_per_seq ? table[tc] : -1;
+            if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, tc);
+            if (tc == colA) s_blk[0] = blk;
+            if (tc == colB) s_blk[1] = blk;
+        }
     }
-    {
+#pragma unroll
+    for (int i = 0; i < kProTokens / 4; ++i) {
         float4 v4;
-        if (pr >= 0 && pr < a.rope_rows) {
+        if (pr[i] >= 0 && pr[i] < a.rope_rows) {
             const float* tab = rsel ? a.sin : a.cos;
-            v4 = *reinterpret_cast<const float4*>(tab + (int64_t)pr * a.rope_stride + rd);
+            v4 = *reinterpret_cast<const float4*>(tab + (int64_t)pr[i] * a.rope_stride + rd);
         } else {  // a position outside the tables: NaN rows
             v4 = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
         }
-        if (rt < ntok) *reinterpret_cast<float4*>(&s_rope[rt][rsel][rd]) = v4;
+        if (rt + 4 * i < ntok) *reinterpret_cast<float4*>(&s_rope[rt + 4 * i][rsel][rd]) = v4;
     }
     float wq[8], wk[8];
     load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
@@ -162,16 +174,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     __syncthreads();
     const int stop = s_stop;
 
-    for (int base = 0; base < pairs; base += 16 * kBatch) {
-        if (base > 0) {
+    // Norm, rotate and store one batch.
+    auto process = [&](int base, const RowRaw<E>(&raw)[kProBatch]) {
 #pragma unroll
-            for (int k = 0; k < kBatch; ++k) {
-                const int pi = base + lrow + 16 * k;
-                if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
+        for (int k = 0; k < kProBatch; ++k) {
             const int pi = base + lrow + 16 * k;  // uniform within the DPP row
             if (pi >= pairs) break;
             const int ti = pi / R;
@@ -219,6 +225,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
             } else if (dst) {
                 store8(E{}, dst, o);
             }
+        }
+    };
+
+    // Two batches in flight: each buffer is refilled as soon as its batch is stored.
+    constexpr int kB = 16 * kProBatch;
+    for (int base = 0; base < pairs; base += 2 * kB) {
+        process(base, ra);
+        if (base + 2 * kB < pairs) load_batch(base + 2 * kB, ra);
+        if (base + kB < pairs) {
+            process(base + kB, rb);
+            if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
         }
     }
 }
