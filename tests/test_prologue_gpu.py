@@ -5,8 +5,8 @@ rotary_embd (QwenRotaryEmbedding, qwen3.py:17-138) and the cache-write loops
 (qwen3.py:240-264, 322-366), restated by oracle.prologue and
 oracle.attention.cache_write.  The kernel computes in fp32 and rounds each
 output once, so q and the written k rows are compared with the float64
-oracle within the storage type's rounding (plus 1e-2 / 1e-4 absolute, the
-north-star tolerances); v rows are copied and must match bit for bit, and
+oracle within the storage type's rounding (plus 1e-2 absolute for bf16 and
+1e-4 for f32, the attention ops' tolerances); v rows are copied and must match bit for bit, and
 every pool byte the reference does not write must keep its (NaN) poison.
 """
 
