@@ -1,7 +1,7 @@
 """CPU oracle for the FemtoVLLM attention hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import this package, and only as the checker (or, for
+``bench.py`` may import this package, and only as the reference for results (or, for
 ``sdpa_path``, as the timed CPU baseline).  The shipped operators never call
 into it; they fail loudly when the HIP library is missing.
 

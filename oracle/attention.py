@@ -1,6 +1,6 @@
 """CPU oracle for the paged-attention hot path -- TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``,
+This module checks results and is never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The shipped operators (``femtovllm.ops`` / ``femtovllm._C``) run
 the HIP kernels in ``libfemto_attn.so`` and raise when that library is absent.

@@ -1,6 +1,6 @@
 """CPU oracle for the attention prologue -- TEST INFRASTRUCTURE ONLY.
 
-The checker of the fused QK-norm + RoPE + cache-write kernel: only
+Reference results for the fused QK-norm + RoPE + cache-write kernel: only
 ``tests/`` and the ``cpu_baseline`` leg of ``bench.py`` may use it; the
 shipped operator runs the HIP kernel in ``libfemto_attn.so``.
 
