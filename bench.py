@@ -120,7 +120,7 @@ def cpu_baseline_decode(w, sample_s=12.0):
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     q, meta = w.gemv_call(device="cpu")
-    args = (q, w.k_pool, w.v_pool, meta.raw_block_tables, meta.raw_kv_lens)
+    args = (q, w.k_pool, w.v_pool, meta.raw_block_tables, meta.kv_lens.tolist())
     sdpa_path.paged_decode(*args)  # warm
     times = []
     t_end = time.perf_counter() + sample_s

@@ -8,7 +8,6 @@
 // index dtype) live in the Python layer that owns the tensors.
 #include <algorithm>
 #include <cmath>
-#include <cstdlib>
 #include <string>
 
 #include "common.h"
@@ -44,13 +43,6 @@ int elem_bytes(int dtype) { return dtype == FEMTO_F32 ? 4 : 2; }
 
 float scale_log2(int head_dim) { return femto::kLog2e / std::sqrt((float)head_dim); }
 
-int env_int(const char* name, int fallback) {
-    const char* s = std::getenv(name);
-    if (!s || !*s) return fallback;
-    const int v = std::atoi(s);
-    return v > 0 ? v : fallback;
-}
-
 }  // namespace
 
 namespace femto {
@@ -62,8 +54,7 @@ DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len) {
     const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
     // A wave's slice is at least min_chunk_pages long, so a sequence is cut
     // into at most max_slots - 1 slices (+1 for a slice straddling its start).
-    p.min_chunk_pages = env_int("FEMTO_DECODE_MIN_CHUNK_PAGES", 0);
-    if (p.min_chunk_pages == 0) p.min_chunk_pages = std::max(4, (max_pages + 31) / 32);
+    p.min_chunk_pages = std::max(4, (max_pages + 31) / 32);
     p.min_chunk_pages = std::max(p.min_chunk_pages, (max_pages + 126) / 127);  // merge kernel: <= 128 slots
     p.max_slots = (max_pages + p.min_chunk_pages - 1) / p.min_chunk_pages + 1;
     return p;

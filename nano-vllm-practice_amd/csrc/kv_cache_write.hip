@@ -15,7 +15,8 @@
 // bytes again.  The copy is bit-exact for every element type.
 //
 // Work: workgroup (x, b) copies tokens q_begin + 4x .. + 3 of sequence b
-// (they span at most two pages).  Each thread moves 16-byte chunks; a
+// (they span at most two pages), then the same four tokens gridDim.x * 4
+// further on, until the sequence ends.  Each thread moves 16-byte chunks; a
 // token is 2 * n_kv_heads * head_dim * element_bytes / 16 chunks (256 for
 // 8 bf16 heads of 128), so one pass of 256 threads x 4 chunks covers the
 // four tokens.  The source rows depend only on cu_seqlens, so their loads
@@ -40,8 +41,10 @@ __global__ __launch_bounds__(256) void kv_cache_write_kernel(CacheWriteArgs a) {
         q_begin = b;
         q_end = b + 1;
     }
-    const int t0 = q_begin + (int)blockIdx.x * kWriteTokens;
-    if (t0 >= q_end) return;
+    // max_q_len only sizes the grid: a sequence longer than it is covered
+    // by later rounds of the same workgroups (the loop condition is uniform
+    // across the workgroup, so the barriers inside stay matched).
+    for (int t0 = q_begin + (int)blockIdx.x * kWriteTokens; t0 < q_end; t0 += (int)gridDim.x * kWriteTokens) {
     const int t1 = min(q_end, t0 + kWriteTokens);
 
     const int cpr = a.row_chunks;         // 16-byte chunks per (token, head) row
@@ -81,6 +84,7 @@ __global__ __launch_bounds__(256) void kv_cache_write_kernel(CacheWriteArgs a) {
             colA = (p0 + (t0 - q_begin)) / kPage;
             const int colB = (p0 + (t1 - 1 - q_begin)) / kPage;  // colA or colA + 1
             const int32_t* table = a.tables + (int64_t)b * a.table_stride;
+            __syncthreads();  // the previous round's readers of s_stop / s_blk are done
             if (threadIdx.x == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
             __syncthreads();
             if (p0 >= 0) {
@@ -115,6 +119,7 @@ __global__ __launch_bounds__(256) void kv_cache_write_kernel(CacheWriteArgs a) {
                 }
             }
         }
+    }
     }
 }
 

@@ -15,7 +15,8 @@
 // caller's fp32 tables (rope_rows, head_dim); a position outside them gives
 // NaN rows, where the reference's index would raise.
 //
-// Work: workgroup (x, b) takes tokens q_begin + 4x .. + 3 of sequence b.
+// Work: workgroup (x, b) takes tokens q_begin + 4x .. + 3 of sequence b,
+// then the four tokens gridDim.x * 4 further on, until the sequence ends.
 // A token has H q rows, KVH k rows and KVH v rows of head_dim = 128; a DPP
 // row of 16 lanes handles one of them, lane c holding dims 8c .. 8c + 7, so
 // the sum of squares is a 16-lane DPP reduction and the RoPE partner of dim
@@ -92,8 +93,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
         q_begin = b;
         q_end = b + 1;
     }
-    const int t0 = q_begin + (int)blockIdx.x * kProTokens;
-    if (t0 >= q_end) return;
+    // max_q_len only sizes the grid: a sequence longer than it is covered
+    // by later rounds of the same workgroups (the loop condition is uniform
+    // across the workgroup, so the barriers inside stay matched).
+    for (int t0 = q_begin + (int)blockIdx.x * kProTokens; t0 < q_end; t0 += (int)gridDim.x * kProTokens) {
     const int t1 = min(q_end, t0 + kProTokens);
     const int ntok = t1 - t0;
     const int tid = threadIdx.x;
@@ -146,6 +149,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int p0 = a.cw.positions[q_begin];
     const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
     const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
+    __syncthreads();  // the previous round's readers of s_stop / s_blk / s_rope are done
     if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
     __syncthreads();
     if (p0 >= 0) {
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
             process(base + kB, rb);
             if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
         }
+    }
     }
 }
 

@@ -20,7 +20,8 @@ reference fails without its compiled extension (femtovllm/ops/__init__.py:6-16).
 Differences from the reference, all supersets: f32 decode is accepted (the
 reference dispatches f16/bf16 only), and the decode kernel splits long
 contexts internally, so ``max_kv_len`` only sizes the split workspace (the
-``kMaxKVLenNonSplit`` check is kept for API parity).
+``kMaxKVLenNonSplit`` check is kept for API parity; ``femtovllm._DEV.split_kv_decode``
+lifts it).  head_dim must be exactly 128 (the reference accepts <= 128).
 """
 
 from __future__ import annotations
@@ -161,17 +162,24 @@ def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q):
     for name, t in (("kv_page_tables", tables), ("kv_lens", kv_lens)):
         _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
     _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}, got {k_pool.size(2)}")
-    _check(q.size(-1) <= kDimHead, f"{fn}: head_dim must be <= {kDimHead}")
+    # The reference accepts head_dim <= 128 (paged_attention_gemv.cu TORCH_CHECK_LE(dim_d, kDimHead)); the
+    # MFMA and wave tilings here are built for exactly 128, the head_dim of every model the engine runs.
+    _check(q.size(-1) == kDimHead, f"{fn}: head_dim must be {kDimHead}, got {q.size(-1)}")
     _check(q.size(0) % k_pool.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
 
 
-def _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len, require_contiguous_q=True):
+def _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len, require_contiguous_q=True,
+                          max_kv_len_limit=kMaxKVLenNonSplit):
+    """Decode through the C ABI.  ``max_kv_len_limit`` is the reference's
+    ``kMaxKVLenNonSplit`` check (paged_attention_gemv.cu:271-274); ``None``
+    lifts it, since the kernel splits contexts of any length over waves."""
     fn = "PagedAttentionGemvCuda"
     _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q)
     n_heads, num_seqs, dim = q.shape
     _check(num_seqs == kv_page_tables.size(0), f"{fn}: q.size(1) must equal kv_page_tables.size(0)")
     _check(num_seqs == kv_lens.size(0), f"{fn}: q.size(1) must equal kv_lens.size(0)")
-    _check(int(max_kv_len) <= kMaxKVLenNonSplit, f"{fn}: max_kv_len {max_kv_len} > kMaxKVLenNonSplit {kMaxKVLenNonSplit}")
+    if max_kv_len_limit is not None:
+        _check(int(max_kv_len) <= max_kv_len_limit, f"{fn}: max_kv_len {max_kv_len} > kMaxKVLenNonSplit {max_kv_len_limit}")
     dtype = _dtype_code(q, fn)
     out = torch.empty((n_heads, num_seqs, dim), dtype=q.dtype, device=q.device)
     if num_seqs == 0:

@@ -7,12 +7,13 @@ kernels for gfx950 from ``libfemto_attn.so``.
 
 ``_DEV`` mirrors the reference's global developer flags
 (femtovllm/__init__.py:7-23): ``ops`` reads ``impl_custom_gemm`` /
-``impl_custom_gemv`` when ``impl`` is not given.
+``impl_custom_gemv`` when ``impl`` is not given, and ``split_kv_decode``
+(the one added flag).
 """
 
 import dataclasses
 
-from femtovllm.protocol import AttentionBackend, ImplCustomKernel
+from femtovllm.protocol import AttentionBackend, ImplCustomKernel, SamplingParams
 
 
 @dataclasses.dataclass
@@ -25,6 +26,14 @@ class DevFlags:
 
     scheduler_version: int = 3
 
+    # Not in the reference: when True, ops.paged_attention_gemv accepts
+    # max_kv_len above MAX_KV_LEN_NON_SPLIT (8192), the limit the reference
+    # leaves "to be implemented" (csrc/utils/constants.cuh:36-39); the HIP
+    # decode kernel splits any context over its waves.  The engine's
+    # HARDWARE_LIMIT (femtovllm/engine/core_engine.py:27) reads the exported
+    # constant, which stays 8192.
+    split_kv_decode: bool = False
+
     @property
     def route_prefill_decode(self) -> bool:
         return self.varlen_attn_backend == AttentionBackend.CUSTOM_GEMM_GEMV
@@ -32,4 +41,4 @@ class DevFlags:
 
 _DEV = DevFlags()
 
-__all__ = ["AttentionBackend", "ImplCustomKernel", "DevFlags", "_DEV"]
+__all__ = ["AttentionBackend", "ImplCustomKernel", "SamplingParams", "DevFlags", "_DEV"]

@@ -6,6 +6,9 @@ model_runner.py:46-72 (tables padded with -1, not 0).  The tensors it returns
 are exactly what ``femtovllm.ops.paged_attention_gemm`` /
 ``paged_attention_gemv`` receive from the engine.
 
+Both return the reference's ``VarlenAttnMetadata`` (femtovllm/protocol.py:58-81,
+mirrored in :mod:`femtovllm.protocol`).
+
 ``build_varlen_metadata_device`` produces the same tensors on the GPU from
 one host-to-device copy of the per-sequence counts and the block tables (CSR)
 and two small kernels, instead of per-token Python lists and one copy per
@@ -14,40 +17,12 @@ tensor; its ``raw_*`` list fields are ``None`` except ``raw_block_tables``.
 
 from __future__ import annotations
 
-import dataclasses
 import itertools
 
 import numpy as np
 import torch
 
-
-@dataclasses.dataclass
-class VarlenMetadata:
-    """The attention fields of the reference's VarlenAttnMetadata (protocol.py:58-81)."""
-
-    positions: torch.Tensor
-    raw_positions: list
-    cu_seqlens: torch.Tensor
-    raw_cu_seqlens: list
-    max_q_len: int
-    Q_TILE_SIZE: int
-    cu_q_tiles: torch.Tensor
-    raw_cu_q_tiles: list
-    q_tile_to_seq_idx: torch.Tensor
-    raw_q_tile_to_seq_idx: list
-    kv_lens: torch.Tensor
-    raw_kv_lens: list
-    max_kv_len: int
-    block_tables: torch.Tensor
-    raw_block_tables: list
-
-    def to(self, device) -> "VarlenMetadata":
-        out = dataclasses.replace(self)
-        for f in dataclasses.fields(self):
-            v = getattr(self, f.name)
-            if isinstance(v, torch.Tensor):
-                setattr(out, f.name, v.to(device))
-        return out
+from femtovllm.protocol import VarlenAttnMetadata
 
 
 def pad_block_tables(raw_block_tables: list) -> list:
@@ -63,7 +38,10 @@ def build_varlen_metadata(
     raw_block_tables: list,
     Q_TILE_SIZE: int = 32,
     device: str | torch.device = "cpu",
-) -> VarlenMetadata:
+    k_cache_pools: list | None = None,
+    v_cache_pools: list | None = None,
+    is_decoding: bool = False,
+) -> VarlenAttnMetadata:
     """Metadata for one prefill (or unified) call.
 
     ``chunks`` holds ``(num_computed_tokens, num_tokens)`` per scheduled
@@ -94,7 +72,7 @@ def build_varlen_metadata(
         return torch.tensor(x, dtype=torch.int32, device=device)
 
     padded = pad_block_tables(raw_block_tables)
-    return VarlenMetadata(
+    return VarlenAttnMetadata(
         positions=i32(raw_positions),
         raw_positions=raw_positions,
         cu_seqlens=i32(raw_cu_seqlens),
@@ -105,11 +83,13 @@ def build_varlen_metadata(
         raw_cu_q_tiles=raw_cu_q_tiles,
         q_tile_to_seq_idx=i32(raw_q_tile_to_seq_idx),
         raw_q_tile_to_seq_idx=raw_q_tile_to_seq_idx,
+        k_cache_pools=list(k_cache_pools or []),
+        v_cache_pools=list(v_cache_pools or []),
         kv_lens=i32(raw_kv_lens),
-        raw_kv_lens=raw_kv_lens,
         max_kv_len=max_kv_len,
         block_tables=torch.tensor(padded, dtype=torch.int32, device=device).reshape(len(padded), -1),
         raw_block_tables=[list(t) for t in raw_block_tables],
+        is_decoding=is_decoding,
     )
 
 
@@ -118,7 +98,10 @@ def build_varlen_metadata_device(
     raw_block_tables: list,
     Q_TILE_SIZE: int = 32,
     device: str | torch.device = "cuda",
-) -> VarlenMetadata:
+    k_cache_pools: list | None = None,
+    v_cache_pools: list | None = None,
+    is_decoding: bool = False,
+) -> VarlenAttnMetadata:
     """``build_varlen_metadata`` with the tensors built by HIP kernels on ``device``.
 
     ``chunks`` holds ``(num_computed_tokens, num_tokens)`` per sequence, as
@@ -148,14 +131,15 @@ def build_varlen_metadata_device(
     flat_len = int(flat.size)
     positions, cu_seqlens, cu_q_tiles, tile_map, kv_lens, tables = _C._build_varlen_metadata(
         packed, num_seqs, flat_len, width, Q_TILE_SIZE, max(max_q_len, 0), total_tokens, total_tiles)
-    return VarlenMetadata(
+    return VarlenAttnMetadata(
         positions=positions, raw_positions=None,
         cu_seqlens=cu_seqlens, raw_cu_seqlens=None,
         max_q_len=max_q_len, Q_TILE_SIZE=Q_TILE_SIZE,
         cu_q_tiles=cu_q_tiles, raw_cu_q_tiles=None,
         q_tile_to_seq_idx=tile_map, raw_q_tile_to_seq_idx=None,
-        kv_lens=kv_lens, raw_kv_lens=None,
-        max_kv_len=max(kv) if kv else -1,
+        k_cache_pools=list(k_cache_pools or []), v_cache_pools=list(v_cache_pools or []),
+        kv_lens=kv_lens, max_kv_len=max(kv) if kv else -1,
         block_tables=tables,
         raw_block_tables=[list(t) for t in raw_block_tables],
+        is_decoding=is_decoding,
     )

@@ -76,6 +76,8 @@ def paged_attention_gemv(
     q (n_heads, num_seqs, head_dim); pools (num_blocks, n_kv_heads, 16,
     head_dim); kv_page_tables (num_seqs, max_pages) int32, -1 padded;
     kv_lens (num_seqs,) int32.  Returns (n_heads, num_seqs, head_dim).
+    ``max_kv_len`` above ``MAX_KV_LEN_NON_SPLIT`` raises ``RuntimeError`` as in
+    the reference unless ``femtovllm._DEV.split_kv_decode`` is set.
     """
     q = _ensure_valid_tensor(q, "q")
 
@@ -90,6 +92,8 @@ def paged_attention_gemv(
             kv_lens,
             max_kv_len,
             require_contiguous_q=False,
+            # getattr: a reference checkout's DevFlags has no such field
+            max_kv_len_limit=None if getattr(femtovllm._DEV, "split_kv_decode", False) else MAX_KV_LEN_NON_SPLIT,
         )
     else:
         raise NotImplementedError()

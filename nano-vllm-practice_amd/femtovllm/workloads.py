@@ -25,7 +25,7 @@ import math
 import numpy as np
 import torch
 
-from femtovllm.metadata import VarlenMetadata, build_varlen_metadata
+from femtovllm.metadata import build_varlen_metadata
 
 PAGE = 16
 

@@ -98,9 +98,9 @@ def gather_seq_kv(pool: np.ndarray, table_row, kv_len: int) -> np.ndarray:
 
 def _softmax_attend(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarray, scale: float):
     """``q`` (Tq, D), ``k``/``v`` (Tk, D), boolean ``mask`` (Tq, Tk)."""
-    q = q.astype(np.float64)
-    k = k.astype(np.float64)
-    v = v.astype(np.float64)
+    q = q.astype(np.float64, copy=False)
+    k = k.astype(np.float64, copy=False)
+    v = v.astype(np.float64, copy=False)
     s = (q @ k.T) * scale
     s = np.where(mask, s, -np.inf)
     with np.errstate(invalid="ignore"):
@@ -131,9 +131,11 @@ def paged_decode(q, k_pool, v_pool, block_tables, kv_lens) -> np.ndarray:
         k = gather_seq_kv(k_pool, block_tables[b], kv_len)
         v = gather_seq_kv(v_pool, block_tables[b], kv_len)
         mask = np.ones((1, kv_len), dtype=bool)
-        for h in range(n_heads):
-            g = kv_head_of(h, n_heads, n_kv)
-            out[h, b] = _softmax_attend(q[h, b : b + 1], k[g], v[g], mask, scale)[0]
+        for g in range(n_kv):
+            kg, vg = k[g].astype(np.float64), v[g].astype(np.float64)
+            for h in range(n_heads):
+                if kv_head_of(h, n_heads, n_kv) == g:
+                    out[h, b] = _softmax_attend(q[h, b : b + 1], kg, vg, mask, scale)[0]
     return out
 
 
@@ -168,9 +170,11 @@ def paged_prefill(
         j = np.arange(kv_len)
         toks = np.asarray(toks)
         mask = visible(j[None, :], kv_len, positions[toks][:, None])
-        for h in range(n_heads):
-            g = kv_head_of(h, n_heads, n_kv)
-            out[h, toks] = _softmax_attend(q[h, toks], k[g], v[g], mask, scale)
+        for g in range(n_kv):
+            kg, vg = k[g].astype(np.float64), v[g].astype(np.float64)
+            for h in range(n_heads):
+                if kv_head_of(h, n_heads, n_kv) == g:
+                    out[h, toks] = _softmax_attend(q[h, toks], kg, vg, mask, scale)
     return out
 
 

@@ -136,18 +136,62 @@ def test_dev_flags_and_enums_mirror_reference():
     assert ImplCustomKernel("cuda") is ImplCustomKernel.CUDA
 
 
+# Every name the reference's engine imports from femtovllm.protocol, by importing module
+# (femtovllm/__init__.py:4, models/qwen/qwen3.py:14, engine/model_runner.py:10,
+# engine/core_engine.py:11, engine/sequence.py:5, engine/scheduler/v3.py:9,
+# engine/kv_cache_manager/v3.py:6, entrypoints/llm.py:10, inputs/input_builder.py:6).
+REFERENCE_PROTOCOL_IMPORTS = {
+    "femtovllm/__init__.py": ["AttentionBackend", "ImplCustomKernel", "SamplingParams"],
+    "femtovllm/models/qwen/qwen3.py": ["AttentionBackend", "VarlenAttnMetadata"],
+    "femtovllm/engine/model_runner.py": ["ImplCustomKernel", "VarlenAttnMetadata"],
+    "femtovllm/engine/core_engine.py": ["ReqId", "SamplingParams", "StepDelta", "StopReason"],
+    "femtovllm/engine/sequence.py": ["ReqId", "SamplingParams", "SeqId", "StopReason"],
+    "femtovllm/engine/scheduler/v3.py": ["StopReason"],
+    "femtovllm/engine/kv_cache_manager/v3.py": ["SeqId"],
+    "femtovllm/entrypoints/llm.py": ["SamplingParams"],
+    "femtovllm/inputs/input_builder.py": ["SamplingParams"],
+}
+
+
+def test_protocol_exports_every_name_the_engine_imports():
+    import dataclasses
+
+    import femtovllm.protocol as P
+
+    for module, names in REFERENCE_PROTOCOL_IMPORTS.items():
+        for n in names:
+            assert hasattr(P, n), f"femtovllm.protocol lacks {n} (imported by {module})"
+    # field names and order of the reference's dataclasses / NamedTuple (protocol.py:35-100)
+    assert [f.name for f in dataclasses.fields(P.VarlenAttnMetadata)] == [
+        "positions", "raw_positions", "cu_seqlens", "raw_cu_seqlens", "max_q_len", "Q_TILE_SIZE",
+        "raw_cu_q_tiles", "cu_q_tiles", "raw_q_tile_to_seq_idx", "q_tile_to_seq_idx", "k_cache_pools",
+        "v_cache_pools", "kv_lens", "max_kv_len", "block_tables", "raw_block_tables", "is_decoding"]
+    assert [f.name for f in dataclasses.fields(P.SamplingParams)] == [
+        "temperature", "presence_penalty", "stop_token_ids", "max_new_tokens"]
+    sp = P.SamplingParams(stop_token_ids=[1, 2])
+    c = sp.clone()
+    assert c == sp and c.stop_token_ids is not sp.stop_token_ids
+    assert P.SamplingParams().max_new_tokens == 5000 and P.SamplingParams().temperature == 1.0
+    assert P.StepDelta._fields == ("req_id", "seq_id", "new_token_id", "stop_reason")
+    assert [m.value for m in P.StopReason] == ["EOS", "LENGTH", "OOM", "HARDWARE_LIMIT"]
+    import femtovllm
+
+    assert femtovllm.SamplingParams is P.SamplingParams
+
+
 def test_metadata_follows_model_runner():
     """femtovllm/engine/model_runner.py:187-202 on the reference test's layout."""
     from femtovllm.metadata import build_varlen_metadata
 
     m = build_varlen_metadata([(51, 8), (28, 16)], [[0, 4, 5, 6], [1, 8, 9]], Q_TILE_SIZE=16)
     assert m.raw_cu_seqlens == [0, 8, 24]
-    assert m.raw_kv_lens == [59, 44]
+    assert m.kv_lens.tolist() == [59, 44]
     assert m.raw_positions == list(range(51, 59)) + list(range(28, 44))
     assert m.raw_cu_q_tiles == [0, 1, 2]
     assert m.raw_q_tile_to_seq_idx == [0, 1]
     assert m.block_tables.tolist() == [[0, 4, 5, 6], [1, 8, 9, -1]]
     assert m.max_q_len == 16 and m.max_kv_len == 59
+    assert not m.is_decoding and m.k_cache_pools == [] and m.v_cache_pools == []
 
 
 def test_workloads_follow_generation_rules():

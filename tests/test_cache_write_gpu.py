@@ -205,3 +205,25 @@ def test_errors(ops, gpu):
         ops.kv_cache_write(k, k, pool, pool, pos[:3], tab[:3])
     with pytest.raises(RuntimeError):  # head count differs from the pools
         ops.kv_cache_write(k[:, :4], k[:, :4], pool, pool, pos, tab)
+
+
+@pytest.mark.parametrize("max_q_len", [1, 5])
+def test_max_q_len_below_chunk_lengths(ops, gpu, max_q_len):
+    """max_q_len only sizes the grid: chunks longer than it are still written whole."""
+    rng = np.random.default_rng(37)
+    prefixes = [0, 17, 200, 5]
+    lens = [70, 1, 33, 129]
+    pages = [-(-(p + n) // 16) for p, n in zip(prefixes, lens)]
+    nb = sum(pages) + 3
+    perm = rng.permutation(nb)
+    tables, at = [], 0
+    for np_ in pages:
+        tables.append([int(x) for x in perm[at:at + np_]])
+        at += np_
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    positions = [p + i for p, n in zip(prefixes, lens) for i in range(n)]
+    k_new, v_new = fresh(rng, cu[-1], 8, 128, torch.bfloat16)
+    run_case(ops, gpu, poisoned_pools(nb, 8, 128, torch.bfloat16), k_new, v_new, tables, cu, positions,
+             max_q_len=max_q_len)

@@ -29,7 +29,7 @@ def run_gemm(ops, q, meta, k_pool, v_pool, device, impl=None):
 
 def oracle_prefill(q, meta, k_pool, v_pool, rows=None):
     return oa.paged_prefill(np64(q), np32(k_pool), np32(v_pool), meta.raw_cu_seqlens, np_tables(meta),
-                            meta.raw_kv_lens, np.asarray(meta.raw_positions), rows=rows)
+                            meta.kv_lens.tolist(), np.asarray(meta.raw_positions), rows=rows)
 
 
 def check_workload(ops, w, gpu, seqs=None, rows_per_seq=None, what=""):
@@ -66,28 +66,71 @@ def test_impl_flag_routes_to_hip(ops, gpu, impl):
 
 
 def test_chunked_prefill_8x512(ops, gpu):
+    """Every one of the 4096 rows of the 8 x 512 chunked batch."""
     w = workloads.prefill_bf16_chunked()
-    err = check_workload(ops, w, gpu, rows_per_seq=48, what="8x512 chunked prefill")
+    err = check_workload(ops, w, gpu, what="8x512 chunked prefill")
     print(f"8x512 max abs err {err:.2e}")
 
 
-@pytest.mark.parametrize("chunk", [0, 7, 15])
-def test_long_context_chunks(ops, gpu, chunk):
+@pytest.fixture(scope="module")
+def long_context(gpu):
+    """The 32k-token Llama-3-8B-shaped sequence, on the host and on the GPU."""
     w = workloads.prefill_bf16_long_llama3_8b()
+    return w, w.to(gpu), np32(w.k_pool), np32(w.v_pool)
+
+
+@pytest.mark.parametrize("chunk", range(16))
+def test_long_context_chunks(ops, gpu, long_context, chunk):
+    """All 16 successive 2048-token chunks, on sampled rows (tile edges included)."""
+    w, wd, kp, vp = long_context
     q, meta = workloads.long_context_chunk(w, chunk, device=gpu)
-    wd = w.to(gpu)
     out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
     rows = sample_rows(meta.raw_cu_seqlens, 24, np.random.default_rng(chunk))
-    want = oracle_prefill(q, meta, w.k_pool, w.v_pool, rows=rows)
+    want = oa.paged_prefill(np64(q), kp, vp, meta.raw_cu_seqlens, np_tables(meta), meta.kv_lens.tolist(),
+                            np.asarray(meta.raw_positions), rows=rows)
     mask = np.zeros(want.shape, dtype=bool)
     mask[:, rows] = True
     assert_close(out, want, torch.bfloat16, f"long-context chunk {chunk}", mask=mask)
 
 
-def test_mixed_batch_single_call(ops, gpu):
-    """One 1024-token chunk on a 4096 prefix plus 127 decode rows in one call, shared blocks."""
+@pytest.fixture(scope="module")
+def mixed(gpu):
+    """The unified Qwen3-8B-shaped batch and the oracle for every row of it.
+
+    Sequence 0 is a 1024-token chunk on a 4096-token prefix, sequences
+    1..127 are decode rows with contexts U[512, 8192]; the even sequences
+    share their first 64 physical blocks.
+    """
     w = workloads.mixed_bf16_qwen3_8b()
-    check_workload(ops, w, gpu, rows_per_seq=2, what="mixed batch")
+    q, meta = w.gemm_call()
+    want = oracle_prefill(q, meta, w.k_pool, w.v_pool)  # (H, 1024 + 127, D), every row
+    return w, w.to(gpu), want
+
+
+def test_mixed_batch_single_call(ops, gpu, mixed):
+    """All 128 sequences in one paged_attention_gemm call (the CUSTOM_GEMM route,
+    femtovllm/models/qwen/qwen3.py:575-580): every prefill and decode row."""
+    w, wd, want = mixed
+    q, meta = w.gemm_call(device=gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    err = assert_close(out, want, torch.bfloat16, "mixed batch, one call")
+    print(f"mixed single call max abs err {err:.2e}")
+
+
+def test_mixed_batch_prefill_plus_decode_route(ops, gpu, mixed):
+    """The reference's default route (femtovllm/engine/model_runner.py:97-141): a
+    paged_attention_gemm call for the chunk and a paged_attention_gemv call for
+    the 127 decode rows (H=32, KVH=8, up to 8192 keys over shared blocks)."""
+    w, wd, want = mixed
+    qp, mp = w.gemm_call(seqs=[0], device=gpu)
+    outp = run_gemm(ops, qp, mp, wd.k_pool, wd.v_pool, gpu)
+    qd, md = w.gemv_call(seqs=range(1, 128), device=gpu)
+    outd = ops.paged_attention_gemv(qd.to(gpu), wd.k_pool, wd.v_pool, md.block_tables, md.kv_lens, md.max_kv_len)
+    torch.cuda.synchronize()
+    assert md.max_kv_len <= 8192
+    e1 = assert_close(outp, want[:, :1024], torch.bfloat16, "mixed route: prefill call")
+    e2 = assert_close(outd, want[:, 1024:], torch.bfloat16, "mixed route: decode call")
+    print(f"mixed route max abs err: prefill {e1:.2e}, decode {e2:.2e}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -84,7 +84,7 @@ def _check(ops, w, gpu, monkeypatch, rows_per_seq=6, what=""):
     assert _workspace_is_zero(gpu), f"workspace not cleared after {what}"
     rows = sample_rows(meta.raw_cu_seqlens, rows_per_seq, np.random.default_rng(1))
     want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), meta.raw_cu_seqlens, np_tables(meta),
-                            meta.raw_kv_lens, np.asarray(meta.raw_positions), rows=rows)
+                            meta.kv_lens.tolist(), np.asarray(meta.raw_positions), rows=rows)
     mask = np.zeros(want.shape, dtype=bool)
     mask[:, rows] = True
     err = assert_close(out, want, w.dtype, what, mask=mask)
@@ -154,7 +154,7 @@ def test_arbitrary_positions_with_split(ops, gpu, monkeypatch):
     rng = np.random.default_rng(92)
     pos = np.asarray(meta.raw_positions).copy()
     s0, s1 = meta.raw_cu_seqlens[0], meta.raw_cu_seqlens[1]
-    pos[s0:s1] = rng.integers(0, meta.raw_kv_lens[0], size=s1 - s0)  # any visible limit inside the context
+    pos[s0:s1] = rng.integers(0, meta.kv_lens.tolist()[0], size=s1 - s0)  # any visible limit inside the context
     meta.raw_positions = [int(x) for x in pos]
     meta.positions = torch.tensor(pos, dtype=torch.int32, device=gpu)
     q = q.to(gpu)
@@ -162,7 +162,7 @@ def test_arbitrary_positions_with_split(ops, gpu, monkeypatch):
     out = _gemm(ops, q, meta, wd)
     assert _workspace_is_zero(gpu)
     want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), meta.raw_cu_seqlens, np_tables(meta),
-                            meta.raw_kv_lens, pos, rows=list(range(s0, s1)))
+                            meta.kv_lens.tolist(), pos, rows=list(range(s0, s1)))
     mask = np.zeros(want.shape, dtype=bool)
     mask[:, s0:s1] = True
     assert_close(out, want, w.dtype, "arbitrary positions, split", mask=mask)

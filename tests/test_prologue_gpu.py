@@ -59,7 +59,7 @@ def make_case(rng, chunks, H, KVH, dtype, tables_extra=3):
     return q, k, v, wq, wk, pool, tab, cu, positions
 
 
-def run_and_check(ops, gpu, case, dtype, decode=False, eps=1e-6, in_place=False):
+def run_and_check(ops, gpu, case, dtype, decode=False, eps=1e-6, in_place=False, max_q_len=None):
     q, k, v, wq, wk, pool, tab, cu, positions = case
     cos, sin = op.rope_tables(8192, 128)
     g = lambda t: t.to(gpu)
@@ -69,7 +69,8 @@ def run_and_check(ops, gpu, case, dtype, decode=False, eps=1e-6, in_place=False)
         qd, g(k), g(v), g(wq), g(wk), eps, g(torch.from_numpy(cos)), g(torch.from_numpy(sin)),
         g(torch.tensor(positions, dtype=torch.int32)), kd, vd, g(tab),
         cu_seqlens=None if decode else g(torch.tensor(cu, dtype=torch.int32)),
-        max_q_len=1 if decode else max(cu[i + 1] - cu[i] for i in range(len(cu) - 1)),
+        max_q_len=max_q_len if max_q_len is not None else
+        (1 if decode else max(cu[i + 1] - cu[i] for i in range(len(cu) - 1))),
         out=qd if in_place else None)
     torch.cuda.synchronize()
     if in_place:
@@ -97,6 +98,14 @@ def test_prefill_chunks(ops, gpu, dtype, heads):
     rng = np.random.default_rng(51 + heads[0])
     chunks = [(int(rng.integers(0, 3000)), int(rng.integers(1, 150))) for _ in range(5)] + [(0, 1), (7000, 33)]
     run_and_check(ops, gpu, make_case(rng, chunks, *heads, dtype), dtype)
+
+
+@pytest.mark.parametrize("max_q_len", [1, 6])
+def test_max_q_len_below_chunk_lengths(ops, gpu, max_q_len):
+    """max_q_len only sizes the grid: chunks longer than it are still processed whole."""
+    rng = np.random.default_rng(55)
+    chunks = [(0, 70), (300, 1), (17, 129), (4000, 33)]
+    run_and_check(ops, gpu, make_case(rng, chunks, 16, 8, torch.bfloat16), torch.bfloat16, max_q_len=max_q_len)
 
 
 def test_decode_layout_in_place(ops, gpu):
