@@ -74,6 +74,30 @@ int femto_paged_attention_gemv(
     void* workspace, size_t workspace_bytes,
     void* stream);
 
+/* femto_paged_attention_gemv without a workspace argument: the partial
+ * softmax states live in a 64 MiB device array of the library (one per GPU,
+ * held until the process ends), so the call allocates nothing and can be
+ * made where hipMalloc cannot (under HIP graph capture, in serving loops
+ * that must not allocate).  No counterpart in the reference; it exists for
+ * those callers.  Limit: two partial states of 130 floats per (sequence,
+ * query head) must fit, i.e. num_seqs * n_heads up to about 64,500 (e.g. 2048
+ * sequences x 32 heads); larger calls fail with FEMTO_ERR_INVALID.  When the default
+ * split does not fit the array, sequences are cut into fewer, longer slices
+ * (same results within rounding; bit-identical where the split is the
+ * same).  All calls on one GPU share the array: calls that may overlap on
+ * one GPU (different streams or threads) race and must be serialised by the
+ * caller. */
+int femto_paged_attention_gemv_noalloc(
+    int dtype,
+    const void* q, int64_t q_stride_head, int64_t q_stride_seq,
+    void* out, int64_t out_stride_head, int64_t out_stride_seq,
+    const void* k_pool, const void* v_pool,
+    int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
+    int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
+    const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+    const int32_t* kv_lens, int num_seqs, int n_heads, int max_kv_len,
+    void* stream);
+
 /* Paged chunked / varlen / causal prefill attention on bf16 or f16 MFMA:
  * token t of sequence b (cu_seqlens[b] <= t < cu_seqlens[b+1]) sees key j
  * iff j < kv_lens[b] and j <= positions[t].

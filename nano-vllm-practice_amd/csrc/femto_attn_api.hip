@@ -8,11 +8,16 @@
 // index dtype) live in the Python layer that owns the tensors.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "common.h"
 #include "femto_attn.h"
 #include "launch.h"
+
+// Scratch of femto_paged_attention_gemv_noalloc (see scratch_pointer below).
+constexpr size_t kScratchBytes = (size_t)64 << 20;  // 64 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
@@ -43,54 +48,7 @@ int elem_bytes(int dtype) { return dtype == FEMTO_F32 ? 4 : 2; }
 
 float scale_log2(int head_dim) { return femto::kLog2e / std::sqrt((float)head_dim); }
 
-}  // namespace
-
-namespace femto {
-
-DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len) {
-    DecodePlan p;
-    const int n_rep = (n_kv_heads > 0) ? n_heads / n_kv_heads : 1;
-    p.nrep_tile = (n_rep % 8 == 0) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
-    const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
-    // A wave's slice is at least min_chunk_pages long, so a sequence is cut
-    // into at most max_slots - 1 slices (+1 for a slice straddling its start).
-    p.min_chunk_pages = std::max(4, (max_pages + 31) / 32);
-    p.min_chunk_pages = std::max(p.min_chunk_pages, (max_pages + 126) / 127);  // merge kernel: <= 128 slots
-    p.max_slots = (max_pages + p.min_chunk_pages - 1) / p.min_chunk_pages + 1;
-    return p;
-}
-
-size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots) {
-    if (num_seqs <= 0) return 0;
-    const size_t slots = (size_t)num_seqs * n_heads * max_slots;
-    size_t bytes = slots * (kDimHead + 2) * sizeof(float);
-    return bytes + (size_t)num_seqs * sizeof(int);
-}
-
-}  // namespace femto
-
-extern "C" {
-
-const char* femto_attn_last_error(void) { return g_err.c_str(); }
-
-int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
-int femto_attn_kv_len_per_page(void) { return femto::kPage; }
-int femto_attn_dim_head(void) { return femto::kDimHead; }
-
-size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
-    if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads) return 0;
-    int resident = 0;
-    if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
-    return femto::prefill_workspace_bytes(resident);
-}
-
-size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
-    if (num_seqs <= 0 || n_heads <= 0) return 0;
-    const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len);
-    return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_slots);
-}
-
-static int check_paged_common(const char* fn, int dtype, const void* q, const void* out, const void* k_pool,
+int check_paged_common(const char* fn, int dtype, const void* q, const void* out, const void* k_pool,
                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
                               int head_dim, int64_t ps0, int64_t ps1, int64_t ps2, int n_heads,
                               int64_t q_s0, int64_t q_s1, const int32_t* tables, int num_pages_per_seq,
@@ -118,29 +76,115 @@ static int check_paged_common(const char* fn, int dtype, const void* q, const vo
     return FEMTO_OK;
 }
 
-int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_seq, void* out,
-                               int64_t out_stride_head, int64_t out_stride_seq, const void* k_pool,
-                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
-                               int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
-                               int64_t pool_stride_row, const int32_t* kv_page_tables, int num_pages_per_seq,
-                               int64_t table_stride, const int32_t* kv_lens, int num_seqs, int n_heads,
-                               int max_kv_len, void* workspace, size_t workspace_bytes, void* stream) {
+// ---- scratch of the allocation-free decode entry point ----------------------
+// femto_paged_attention_gemv_noalloc keeps its partial softmax states here
+// instead of a caller workspace: a file-scope device array, one copy per GPU
+// the library runs on, held until the process ends.  Host code never uses the
+// array's name as an address (on the host it names a stand-in, not device
+// memory); the device address comes from hipGetSymbolAddress, once per device
+// on the entry point's first call there, and only that pointer reaches the
+// kernels.  Every call on one GPU shares the array (it keeps the last call's
+// contents; decode needs no zero-filled state), so calls that may overlap on
+// one GPU (other streams, other threads) race.
+// (The array itself is declared at file scope above this namespace.)
+// Largest num_seqs * n_heads that still fits two partial slots per (sequence,
+// head): (64 MiB) / (2 * 130 floats) ~ 64.5 k, e.g. 2048 sequences x 32 heads.
+constexpr int64_t kScratchMaxSeqHeads = (int64_t)(kScratchBytes / (2 * (femto::kDimHead + 2) * sizeof(float)));
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up on first use.
+int scratch_pointer(const std::string& fn, void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, (fn + ": hipGetDevice").c_str());
+    if (dev < 0 || dev >= kMaxDevices) return fail(FEMTO_ERR_UNSUPPORTED, fn + ": device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, (fn + ": hipGetSymbolAddress(scratch)").c_str());
+        if (!p) return fail(FEMTO_ERR_HIP, fn + ": hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return FEMTO_OK;
+}
+
+}  // namespace
+
+namespace femto {
+
+DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len) {
+    DecodePlan p;
+    const int n_rep = (n_kv_heads > 0) ? n_heads / n_kv_heads : 1;
+    p.nrep_tile = (n_rep % 8 == 0) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
+    const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
+    // A wave's slice is at least min_chunk_pages long, so a sequence is cut
+    // into at most max_slots - 1 slices (+1 for a slice straddling its start).
+    p.min_chunk_pages = std::max(4, (max_pages + 31) / 32);
+    p.min_chunk_pages = std::max(p.min_chunk_pages, (max_pages + 126) / 127);  // merge kernel: <= 128 slots
+    p.max_slots = (max_pages + p.min_chunk_pages - 1) / p.min_chunk_pages + 1;
+    return p;
+}
+
+size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots) {
+    if (num_seqs <= 0) return 0;
+    const size_t slots = (size_t)num_seqs * n_heads * max_slots;
+    size_t bytes = slots * (kDimHead + 2) * sizeof(float);
+    return bytes + (size_t)num_seqs * sizeof(int);
+}
+
+}  // namespace femto
+
+// Decode entry points: femto_paged_attention_gemv (workspace from the caller)
+// and femto_paged_attention_gemv_noalloc (workspace = this device's scratch).
+static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int64_t q_stride_head,
+                              int64_t q_stride_seq, void* out, int64_t out_stride_head, int64_t out_stride_seq,
+                              const void* k_pool, const void* v_pool, int64_t num_blocks, int n_kv_heads,
+                              int block_size, int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
+                              int64_t pool_stride_row, const int32_t* kv_page_tables, int num_pages_per_seq,
+                              int64_t table_stride, const int32_t* kv_lens, int num_seqs, int n_heads, int max_kv_len,
+                              bool use_scratch, void* workspace, size_t workspace_bytes, void* stream) {
     g_err.clear();
+    const std::string fn(fn_name);
     if (dtype != FEMTO_F32 && dtype != FEMTO_F16 && dtype != FEMTO_BF16)
-        return fail(FEMTO_ERR_UNSUPPORTED, std::string("paged_attention_gemv: dtype ") + dtype_name(dtype) +
-                                               " is not supported");
-    if (num_seqs < 0 || max_kv_len < 0) return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: negative size");
+        return fail(FEMTO_ERR_UNSUPPORTED, fn + ": dtype " + dtype_name(dtype) + " is not supported");
+    if (num_seqs < 0 || max_kv_len < 0) return fail(FEMTO_ERR_INVALID, fn + ": negative size");
     if (num_seqs == 0) return FEMTO_OK;
-    if (!kv_lens) return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: null kv_lens");
-    int rc = check_paged_common("paged_attention_gemv", dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
+    if (!kv_lens) return fail(FEMTO_ERR_INVALID, fn + ": null kv_lens");
+    int rc = check_paged_common(fn_name, dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
                                 block_size, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, n_heads,
                                 q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride);
     if (rc != FEMTO_OK) return rc;
 
-    const femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len);
+    femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len);
+    if (use_scratch) {
+        // The partial slots must fit the scratch array: with fewer slots per
+        // (sequence, head) a sequence is cut into fewer, longer slices (the
+        // kernel sizes slices from the longest sequence and max_slots).
+        const size_t per_slot = (size_t)num_seqs * n_heads * (femto::kDimHead + 2) * sizeof(float);
+        const size_t fixed = (size_t)num_seqs * sizeof(int);
+        const size_t fit = kScratchBytes > fixed ? (kScratchBytes - fixed) / per_slot : 0;
+        if (fit < 2)
+            return fail(FEMTO_ERR_INVALID,
+                        fn + ": num_seqs * n_heads = " + std::to_string((int64_t)num_seqs * n_heads) +
+                            " exceeds the scratch limit of " + std::to_string(kScratchMaxSeqHeads) +
+                            " (sequences x query heads); use femto_paged_attention_gemv with a workspace");
+        if ((size_t)plan.max_slots > fit) {
+            const int max_pages = max_kv_len > 0 ? (max_kv_len + femto::kPage - 1) / femto::kPage : 1;
+            plan.max_slots = (int)fit;
+            plan.min_chunk_pages = std::max(plan.min_chunk_pages, (max_pages + plan.max_slots - 2) / (plan.max_slots - 1));
+        }
+        rc = scratch_pointer(fn, &workspace);
+        if (rc != FEMTO_OK) return rc;
+        workspace_bytes = kScratchBytes;
+    }
     const size_t need = femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_slots);
     if (!workspace || workspace_bytes < need || !aligned(workspace, 256))
-        return fail(FEMTO_ERR_INVALID, "paged_attention_gemv: workspace of " + std::to_string(need) +
+        return fail(FEMTO_ERR_INVALID, fn + ": workspace of " + std::to_string(need) +
                                            " bytes (256-byte aligned) required, got " +
                                            std::to_string(workspace_bytes));
 
@@ -174,7 +218,58 @@ int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, 
     a.part_ml = a.part_acc + slots * femto::kDimHead;
     a.seq_slots = reinterpret_cast<int*>(a.part_ml + slots * 2);
     return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, static_cast<hipStream_t>(stream)),
-                      "paged_attention_gemv launch");
+                      (fn + " launch").c_str());
+}
+
+extern "C" {
+
+const char* femto_attn_last_error(void) { return g_err.c_str(); }
+
+int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
+int femto_attn_kv_len_per_page(void) { return femto::kPage; }
+int femto_attn_dim_head(void) { return femto::kDimHead; }
+
+size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
+    if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads) return 0;
+    int resident = 0;
+    if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
+    return femto::prefill_workspace_bytes(resident);
+}
+
+size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
+    if (num_seqs <= 0 || n_heads <= 0) return 0;
+    const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len);
+    return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_slots);
+}
+
+
+int femto_paged_attention_gemv(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_seq, void* out,
+                               int64_t out_stride_head, int64_t out_stride_seq, const void* k_pool,
+                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
+                               int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
+                               int64_t pool_stride_row, const int32_t* kv_page_tables, int num_pages_per_seq,
+                               int64_t table_stride, const int32_t* kv_lens, int num_seqs, int n_heads,
+                               int max_kv_len, void* workspace, size_t workspace_bytes, void* stream) {
+    return paged_decode_entry("paged_attention_gemv", dtype, q, q_stride_head, q_stride_seq, out, out_stride_head,
+                              out_stride_seq, k_pool, v_pool, num_blocks, n_kv_heads, block_size, head_dim,
+                              pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables,
+                              num_pages_per_seq, table_stride, kv_lens, num_seqs, n_heads, max_kv_len, false,
+                              workspace, workspace_bytes, stream);
+}
+
+int femto_paged_attention_gemv_noalloc(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_seq,
+                                       void* out, int64_t out_stride_head, int64_t out_stride_seq,
+                                       const void* k_pool, const void* v_pool, int64_t num_blocks, int n_kv_heads,
+                                       int block_size, int head_dim, int64_t pool_stride_block,
+                                       int64_t pool_stride_head, int64_t pool_stride_row,
+                                       const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
+                                       const int32_t* kv_lens, int num_seqs, int n_heads, int max_kv_len,
+                                       void* stream) {
+    return paged_decode_entry("paged_attention_gemv_noalloc", dtype, q, q_stride_head, q_stride_seq, out,
+                              out_stride_head, out_stride_seq, k_pool, v_pool, num_blocks, n_kv_heads, block_size,
+                              head_dim, pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables,
+                              num_pages_per_seq, table_stride, kv_lens, num_seqs, n_heads, max_kv_len, true, nullptr,
+                              0, stream);
 }
 
 int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, int64_t q_stride_token, void* out,

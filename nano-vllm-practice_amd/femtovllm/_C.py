@@ -53,6 +53,10 @@ def _load() -> ctypes.CDLL:
     lib.femto_paged_attention_gemv.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i64, p, i, i, i, p, sz, p,
     ]
+    lib.femto_paged_attention_gemv_noalloc.restype = i
+    lib.femto_paged_attention_gemv_noalloc.argtypes = [
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i64, p, i, i, i, p,
+    ]
     lib.femto_paged_attention_gemm.restype = i
     lib.femto_paged_attention_gemm.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p, sz, p,
