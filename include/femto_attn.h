@@ -108,13 +108,24 @@ int femto_paged_attention_gemv_noalloc(
  * called by femtovllm.ops.paged_attention_gemm (femtovllm/ops/__init__.py:110-156).
  * dtype: F16 or BF16 (the reference kernels reject F32 too).  A row with
  * no visible key (kv_len == 0) is NaN, as in the reference.
+ * max_q_len: the longest sequence's token count, as the reference binding
+ * takes it; it only bounds how many sequences may have exactly one token.
  * workspace may be NULL.  With a workspace of at least
- * femto_paged_attention_gemm_workspace_size() bytes (256-byte aligned,
- * zero-filled before its first use; every call leaves it zero-filled), the
- * query tiles of sequences much longer than the average are split over
- * their keys and merged within the launch, so a few long sequences do not
- * set the length of the call.  Calls that may overlap (other streams) must
- * not share a workspace. */
+ * femto_paged_attention_gemm_workspace_size() bytes (256-byte aligned; its
+ * first femto_paged_attention_gemm_split_bytes() bytes zero-filled before
+ * the first use, and every call leaves them zero-filled):
+ *  - the query tiles of sequences much longer than the average are split
+ *    over their keys and merged within the launch, so a few long sequences
+ *    do not set the length of the call;
+ *  - when num_seqs, num_tokens and max_q_len allow sequences of one query
+ *    token (decode rows of a mixed batch), those rows run on the decode
+ *    kernel's wave workers (the rest of the workspace holds their partial
+ *    states) and the MFMA tiles skip them; the workers share the tiles'
+ *    launch (a separate decode launch first when n_heads / n_kv_heads is a
+ *    multiple of 8) and a small merge launch follows.  Without a workspace
+ *    the MFMA kernel computes every row.
+ * Every launch goes on `stream`.  Calls that may overlap (other streams)
+ * must not share a workspace. */
 int femto_paged_attention_gemm(
     int dtype,
     const void* q, int64_t q_stride_head, int64_t q_stride_token,
@@ -122,18 +133,26 @@ int femto_paged_attention_gemm(
     const void* k_pool, const void* v_pool,
     int64_t num_blocks, int n_kv_heads, int block_size, int head_dim,
     int64_t pool_stride_block, int64_t pool_stride_head, int64_t pool_stride_row,
-    const int32_t* cu_seqlens, int num_seqs, int num_tokens, int n_heads,
+    const int32_t* cu_seqlens, int num_seqs, int num_tokens, int max_q_len, int n_heads,
     const int32_t* kv_page_tables, int num_pages_per_seq, int64_t table_stride,
     const int32_t* kv_lens, const int32_t* positions,
     void* workspace, size_t workspace_bytes,
     void* stream);
 
-/* Bytes of the optional key-split workspace of femto_paged_attention_gemm:
- * one counter and one 66 KiB partial slot per workgroup the current device
- * holds at once (2 per CU), independent of the batch; 0 for an empty call or
- * without a device.  No counterpart in the reference, whose prefill kernels
- * take no workspace. */
-size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads);
+/* Bytes of the optional workspace of femto_paged_attention_gemm: the
+ * key-split part (one counter and one 66 KiB partial slot per workgroup the
+ * current device holds at once, 2 per CU, independent of the batch) plus,
+ * when the sizes allow one-token sequences, the decode rows' partial states
+ * (num_seqs x n_heads x slots of 130 floats, slots set by the table width
+ * num_pages_per_seq); 0 for an empty call or without a device.  No
+ * counterpart in the reference, whose prefill kernels take no workspace. */
+size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int max_q_len, int n_heads,
+                                                 int n_kv_heads, int num_pages_per_seq);
+
+/* Leading bytes of that workspace that must be zero-filled before its first
+ * use (the key-split counters and partial slots; the decode-row part needs no
+ * initialisation).  No counterpart in the reference. */
+size_t femto_paged_attention_gemm_split_bytes(void);
 
 /* KV-cache write: scatter new K/V rows into the paged pools, bit-exact.
  * k, v: (num_tokens, n_kv_heads, head_dim), element strides per token and

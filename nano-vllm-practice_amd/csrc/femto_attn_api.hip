@@ -117,10 +117,11 @@ int scratch_pointer(const std::string& fn, void** ptr) {
 
 namespace femto {
 
-DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len) {
+DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len, int dtype) {
     DecodePlan p;
     const int n_rep = (n_kv_heads > 0) ? n_heads / n_kv_heads : 1;
-    p.nrep_tile = (n_rep % 8 == 0) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
+    // f32 pages take twice the registers: at most 4 query heads per wave
+    p.nrep_tile = (n_rep % 8 == 0 && dtype != kDtypeF32) ? 8 : (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1;
     const int max_pages = max_kv_len > 0 ? (max_kv_len + kPage - 1) / kPage : 1;
     // A wave's slice is at least min_chunk_pages long, so a sequence is cut
     // into at most max_slots - 1 slices (+1 for a slice straddling its start).
@@ -135,6 +136,60 @@ size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots) {
     const size_t slots = (size_t)num_seqs * n_heads * max_slots;
     size_t bytes = slots * (kDimHead + 2) * sizeof(float);
     return bytes + (size_t)num_seqs * sizeof(int);
+}
+
+// Kernel arguments of a decode launch over the pools; q rows / out rows b
+// (decode call) or cu_seqlens[b] (decode rows of a prefill call).
+DecodeArgs decode_args(const DecodePlan& plan, const void* q, int64_t q_stride_head, int64_t q_stride_row, void* out,
+                       int64_t out_stride_head, int64_t out_stride_row, const void* k_pool, const void* v_pool,
+                       int64_t num_blocks, int n_kv_heads, int head_dim, int64_t pool_stride_block,
+                       int64_t pool_stride_head, int64_t pool_stride_row, const int32_t* kv_page_tables,
+                       int num_pages_per_seq, int64_t table_stride, const int32_t* kv_lens, int num_seqs, int n_heads,
+                       void* workspace) {
+    DecodeArgs a{};
+    a.q = q;
+    a.q_stride_head = q_stride_head;
+    a.q_stride_seq = q_stride_row;
+    a.out = out;
+    a.out_stride_head = out_stride_head;
+    a.out_stride_seq = out_stride_row;
+    a.k_pool = k_pool;
+    a.v_pool = v_pool;
+    a.num_blocks = num_blocks;
+    a.pool_stride_block = pool_stride_block;
+    a.pool_stride_head = pool_stride_head;
+    a.pool_stride_row = pool_stride_row;
+    a.tables = kv_page_tables;
+    a.table_stride = table_stride;
+    a.num_pages_per_seq = num_pages_per_seq;
+    a.kv_lens = kv_lens;
+    a.n_heads = n_heads;
+    a.n_rep = n_heads / n_kv_heads;
+    a.head_groups = a.n_rep / plan.nrep_tile;
+    a.num_seqs = num_seqs;
+    a.grid_heads = n_heads / plan.nrep_tile;
+    a.min_chunk_pages = plan.min_chunk_pages;
+    a.max_slots = plan.max_slots;
+    a.scale_log2 = ::scale_log2(head_dim);
+    const size_t slots = (size_t)num_seqs * n_heads * plan.max_slots;
+    a.part_acc = static_cast<float*>(workspace);
+    a.part_ml = a.part_acc + slots * kDimHead;
+    a.seq_slots = reinterpret_cast<int*>(a.part_ml + slots * 2);
+    return a;
+}
+
+// Upper bound on the sequences of exactly one query token in a varlen call of
+// num_seqs sequences, num_tokens tokens and at most max_q_len tokens each:
+// with d such sequences, num_tokens <= d + (num_seqs - d) * max_q_len.  Zero
+// proves there are none (e.g. every chunked prefill call of full chunks), and
+// then no decode launch is made.  The bound only decides whether to launch:
+// when it is positive the decode kernel takes every one-token sequence, and
+// when a max_q_len below the longest chunk makes it zero the prefill kernel
+// keeps every row itself, so either way each row is computed once.
+int decode_rows_bound(int num_seqs, int num_tokens, int max_q_len) {
+    if (max_q_len <= 1) return num_seqs;
+    const int64_t d = ((int64_t)num_seqs * max_q_len - num_tokens) / (max_q_len - 1);
+    return (int)std::max<int64_t>(0, std::min<int64_t>(num_seqs, d));
 }
 
 }  // namespace femto
@@ -160,7 +215,7 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
                                 q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride);
     if (rc != FEMTO_OK) return rc;
 
-    femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len);
+    femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len, dtype);
     if (use_scratch) {
         // The partial slots must fit the scratch array: with fewer slots per
         // (sequence, head) a sequence is cut into fewer, longer slices (the
@@ -188,37 +243,26 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
                                            " bytes (256-byte aligned) required, got " +
                                            std::to_string(workspace_bytes));
 
-    femto::DecodeArgs a{};
-    a.q = q;
-    a.q_stride_head = q_stride_head;
-    a.q_stride_seq = q_stride_seq;
-    a.out = out;
-    a.out_stride_head = out_stride_head;
-    a.out_stride_seq = out_stride_seq;
-    a.k_pool = k_pool;
-    a.v_pool = v_pool;
-    a.num_blocks = num_blocks;
-    a.pool_stride_block = pool_stride_block;
-    a.pool_stride_head = pool_stride_head;
-    a.pool_stride_row = pool_stride_row;
-    a.tables = kv_page_tables;
-    a.table_stride = table_stride;
-    a.num_pages_per_seq = num_pages_per_seq;
-    a.kv_lens = kv_lens;
-    a.n_heads = n_heads;
-    a.n_rep = n_heads / n_kv_heads;
-    a.head_groups = a.n_rep / plan.nrep_tile;
-    a.num_seqs = num_seqs;
-    a.grid_heads = n_heads / plan.nrep_tile;
-    a.min_chunk_pages = plan.min_chunk_pages;
-    a.max_slots = plan.max_slots;
-    a.scale_log2 = scale_log2(head_dim);
-    const size_t slots = (size_t)num_seqs * n_heads * plan.max_slots;
-    a.part_acc = static_cast<float*>(workspace);
-    a.part_ml = a.part_acc + slots * femto::kDimHead;
-    a.seq_slots = reinterpret_cast<int*>(a.part_ml + slots * 2);
+    const femto::DecodeArgs a = femto::decode_args(
+        plan, q, q_stride_head, q_stride_seq, out, out_stride_head, out_stride_seq, k_pool, v_pool, num_blocks,
+        n_kv_heads, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables, num_pages_per_seq,
+        table_stride, kv_lens, num_seqs, n_heads, workspace);
     return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, static_cast<hipStream_t>(stream)),
                       (fn + " launch").c_str());
+}
+
+// Decode-row part of a prefill call's workspace (after the key-split part):
+// the decode kernel's partial slots for every sequence, sized for the table
+// width, when the call may hold sequences of one query token.
+static femto::DecodePlan gemm_decode_plan(int n_heads, int n_kv_heads, int num_pages_per_seq) {
+    const int64_t max_kv = std::min<int64_t>((int64_t)num_pages_per_seq * femto::kPage, 1 << 30);
+    return femto::plan_paged_decode(n_heads, n_kv_heads, (int)std::max<int64_t>(1, max_kv), femto::kDtypeBF16);
+}
+static size_t gemm_decode_bytes(int num_seqs, int num_tokens, int max_q_len, int n_heads, int n_kv_heads,
+                                int num_pages_per_seq) {
+    if (femto::decode_rows_bound(num_seqs, num_tokens, max_q_len) == 0) return 0;
+    const femto::DecodePlan plan = gemm_decode_plan(n_heads, n_kv_heads, num_pages_per_seq);
+    return (femto::decode_workspace_bytes(num_seqs, n_heads, plan.max_slots) + 255) & ~(size_t)255;
 }
 
 extern "C" {
@@ -229,8 +273,16 @@ int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
 int femto_attn_kv_len_per_page(void) { return femto::kPage; }
 int femto_attn_dim_head(void) { return femto::kDimHead; }
 
-size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int n_heads, int n_kv_heads) {
+size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int max_q_len, int n_heads,
+                                                 int n_kv_heads, int num_pages_per_seq) {
     if (num_seqs <= 0 || num_tokens <= 0 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads) return 0;
+    int resident = 0;
+    if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
+    return femto::prefill_workspace_bytes(resident) +
+           gemm_decode_bytes(num_seqs, num_tokens, max_q_len, n_heads, n_kv_heads, num_pages_per_seq);
+}
+
+size_t femto_paged_attention_gemm_split_bytes(void) {
     int resident = 0;
     if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
     return femto::prefill_workspace_bytes(resident);
@@ -238,7 +290,7 @@ size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, i
 
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {
     if (num_seqs <= 0 || n_heads <= 0) return 0;
-    const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len);
+    const femto::DecodePlan p = femto::plan_paged_decode(n_heads, 1, max_kv_len, femto::kDtypeBF16);  // slots only
     return femto::decode_workspace_bytes(num_seqs, n_heads, p.max_slots);
 }
 
@@ -277,14 +329,15 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
                                const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
                                int head_dim, int64_t pool_stride_block, int64_t pool_stride_head,
                                int64_t pool_stride_row, const int32_t* cu_seqlens, int num_seqs, int num_tokens,
-                               int n_heads, const int32_t* kv_page_tables, int num_pages_per_seq,
+                               int max_q_len, int n_heads, const int32_t* kv_page_tables, int num_pages_per_seq,
                                int64_t table_stride, const int32_t* kv_lens, const int32_t* positions,
                                void* workspace, size_t workspace_bytes, void* stream) {
     g_err.clear();
     if (dtype != FEMTO_F16 && dtype != FEMTO_BF16)
         return fail(FEMTO_ERR_UNSUPPORTED, std::string("paged_attention_gemm: not implemented for '") +
                                                dtype_name(dtype) + "' (bf16 / f16 MFMA only)");
-    if (num_seqs < 0 || num_tokens < 0) return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: negative size");
+    if (num_seqs < 0 || num_tokens < 0 || max_q_len < 0)
+        return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: negative size");
     if (num_seqs == 0 || num_tokens == 0) return FEMTO_OK;
     if (!cu_seqlens || !kv_lens || !positions)
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: null cu_seqlens / kv_lens / positions");
@@ -323,20 +376,51 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
     a.n_kv_heads = n_kv_heads;
     a.n_rep = n_heads / n_kv_heads;
     a.scale_log2 = scale_log2(head_dim);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int decode_rows = 0;
     if (workspace) {
         int resident = 0;
         rc = hip_status(femto::prefill_resident_workgroups(resident), "paged_attention_gemm: device query");
         if (rc != FEMTO_OK) return rc;
-        const size_t need = femto::prefill_workspace_bytes(resident);
+        const size_t split_bytes = femto::prefill_workspace_bytes(resident);
+        const size_t need = split_bytes + gemm_decode_bytes(num_seqs, num_tokens, max_q_len, n_heads, n_kv_heads,
+                                                            num_pages_per_seq);
         if (workspace_bytes < need || !aligned(workspace, 256))
             return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: workspace of " + std::to_string(need) +
                                                " bytes (256-byte aligned) required, got " +
                                                std::to_string(workspace_bytes));
         a.counters = static_cast<int*>(workspace);
         a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + femto::prefill_counter_bytes(resident));
+        if (need > split_bytes) {
+            // Sequences of one query token (decode rows of a mixed batch) run
+            // on the decode kernel's wave workers, which stream their pages at
+            // HBM speed (an MFMA tile would hold one valid row of 32).  When
+            // the workers take as many query heads per wave as a tile takes
+            // (every head ratio but multiples of 8) they run in the same
+            // launch as the tiles, which fill the CU slots beside them; else
+            // the decode kernel runs first.
+            const femto::DecodePlan plan = gemm_decode_plan(n_heads, n_kv_heads, num_pages_per_seq);
+            femto::DecodeArgs d = femto::decode_args(
+                plan, q, q_stride_head, q_stride_token, out, out_stride_head, out_stride_token, k_pool, v_pool,
+                num_blocks, n_kv_heads, head_dim, pool_stride_block, pool_stride_head, pool_stride_row,
+                kv_page_tables, num_pages_per_seq, table_stride, kv_lens, num_seqs, n_heads,
+                static_cast<char*>(workspace) + split_bytes);
+            d.cu_seqlens = cu_seqlens;
+            d.positions = positions;
+            a.skip_decode_rows = 1;
+            decode_rows = femto::decode_rows_bound(num_seqs, num_tokens, max_q_len);
+            if (plan.nrep_tile == femto::prefill_group(a.n_rep)) {
+                a.decode_blocks = femto::decode_worker_blocks(d);
+                if (a.decode_blocks <= 0) return fail(FEMTO_ERR_HIP, "paged_attention_gemm: device query");
+                a.dec = d;
+            } else {
+                rc = hip_status(femto::launch_paged_decode(dtype, d, plan.nrep_tile, num_seqs, st),
+                                "paged_attention_gemm decode-row launch");
+                if (rc != FEMTO_OK) return rc;
+            }
+        }
     }
-    return hip_status(femto::launch_paged_prefill(dtype, a, num_tokens, static_cast<hipStream_t>(stream)),
-                      "paged_attention_gemm launch");
+    return hip_status(femto::launch_paged_prefill(dtype, a, num_tokens, decode_rows, st), "paged_attention_gemm launch");
 }
 
 int femto_kv_cache_write(int dtype, const void* k, int64_t k_stride_token, int64_t k_stride_head, const void* v,

@@ -31,6 +31,12 @@ struct DecodeArgs {
     float* part_acc;  // [num_seqs][n_heads][max_slots][128]
     float* part_ml;   // [num_seqs][n_heads][max_slots][2]
     int* seq_slots;   // [num_seqs] partial slots written for the sequence
+    // Decode rows of a varlen prefill call (both null for a decode call):
+    // sequence b takes part iff it has exactly one query token, that token
+    // is row cu_seqlens[b] of q and out, and it sees keys
+    // j < min(kv_lens[b], positions[row] + 1).
+    const int32_t* cu_seqlens;
+    const int32_t* positions;
 };
 
 // Work split of a decode call.
@@ -39,10 +45,14 @@ struct DecodePlan {
     int min_chunk_pages;  // pages
     int max_slots;
 };
-DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len);
+DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len, int dtype);
 size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots);
 
 hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st);
+// Decode workers of a fused prefill launch: workgroups needed (sets
+// a.waves_per_group; 0 on a device error), and the merge that follows.
+int decode_worker_blocks(DecodeArgs& a);
+hipError_t launch_paged_decode_merge(int dtype, const DecodeArgs& a, int num_seqs, hipStream_t st);
 
 struct PrefillArgs {
     const void* q;
@@ -73,6 +83,12 @@ struct PrefillArgs {
     int* counters;        // one arrival counter per resident workgroup
     int items_per_group;  // upper bound on query tiles per (kv head, head group)
     int resident;         // workgroups the GPU holds at once
+    int skip_decode_rows; // sequences of one query token are left to the decode workers
+    // Decode workers in the same launch (paged only): the first decode_blocks
+    // workgroups run the decode kernel's waves over `dec` (one-token
+    // sequences), the rest the MFMA tiles; 0: none.
+    int decode_blocks;
+    DecodeArgs dec;
 };
 
 // Key split: at most kMaxPieces pieces per query tile, each leaving a
@@ -146,7 +162,12 @@ struct MetadataArgs {
 
 hipError_t launch_varlen_metadata(const MetadataArgs& a, int max_q_len, hipStream_t st);
 
-hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st);
+// decode_rows_max: upper bound on the one-token sequences when
+// a.skip_decode_rows is set (0 otherwise).  With a.decode_blocks > 0 the
+// decode workers run in the same launch (a.dec's head groups must hold
+// prefill_group(n_rep) heads each) and the merge follows on `st`.
+hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, int decode_rows_max, hipStream_t st);
+int prefill_group(int n_rep);
 hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st);
 
 }  // namespace femto

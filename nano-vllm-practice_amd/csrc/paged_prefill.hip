@@ -43,9 +43,11 @@
 //    output.  Only the partials bypass the caches, so no cache-wide
 //    write-back or invalidate is needed.  The last piece also resets the
 //    counter and clears the slots, leaving the workspace all zeros.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
+#include "decode_worker.h"
 #include "launch.h"
 
 namespace femto {
@@ -150,7 +152,7 @@ __device__ __forceinline__ int block_incl_scan(int v, int* s_red, int& total) {
     return v + off;
 }
 
-template <typename E, int G, bool PAGED>
+template <typename E, int G, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_mfma_kernel(PrefillArgs a) {
     constexpr int EB = 2;
     constexpr int BT = 32 * (4 / G);
@@ -169,7 +171,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // ---- work item, XCD-aware: workgroup id mod 8 selects the XCD, and
     // each XCD takes a contiguous range of the work list (KV head groups
     // outermost, so a head's pages stay in one L2).
-    const int lin = blockIdx.x;
+    int lin = blockIdx.x;
+    if constexpr (FUSED) {
+        // The first workgroups are decode workers (G query heads per wave, as
+        // the decode kernel would use for this head ratio); they are
+        // dispatched first, one per CU, and the tiles fill the other slots.
+        if (lin < a.decode_blocks) {
+            decode_waves<E, G>(a.dec, lin);
+            return;
+        }
+        lin -= a.decode_blocks;  // a multiple of 8: the XCD of a tile is unchanged
+    }
     int grp, tile_lin;
     int b, tile, q_begin, q_end, kv_len;
     // Key split of this query tile: piece `piece` of `npieces`; its siblings
@@ -185,6 +197,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (tid < a.num_seqs) {
             my_q0 = a.cu_seqlens[tid];
             my_ql = a.cu_seqlens[tid + 1] - my_q0;
+            if (a.skip_decode_rows && my_ql == 1) my_ql = 0;  // run by the decode kernel
             my_kvl = a.kv_lens[tid];
         }
         auto seq_sizes = [&](int i, int& ql, int& kvl) {
@@ -193,6 +206,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 kvl = my_kvl;
             } else {
                 ql = a.cu_seqlens[i + 1] - a.cu_seqlens[i];
+                if (a.skip_decode_rows && ql == 1) ql = 0;
                 kvl = a.kv_lens[i];
             }
         };
@@ -802,16 +816,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 static int pick_group(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
-template <typename E, bool PAGED>
-static hipError_t launch_g(int G, const PrefillArgs& a, hipStream_t st) {
-    const int grid = ((a.total_work + 7) / 8) * 8;
+template <typename E, bool PAGED, bool FUSED>
+static hipError_t launch_gf(int G, const PrefillArgs& a, hipStream_t st) {
+    const int grid = (FUSED ? a.decode_blocks : 0) + ((a.total_work + 7) / 8) * 8;
     switch (G) {
-        case 1: hipLaunchKernelGGL((attention_mfma_kernel<E, 1, PAGED>), dim3(grid), dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attention_mfma_kernel<E, 2, PAGED>), dim3(grid), dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attention_mfma_kernel<E, 4, PAGED>), dim3(grid), dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((attention_mfma_kernel<E, 1, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((attention_mfma_kernel<E, 2, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((attention_mfma_kernel<E, 4, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <typename E, bool PAGED>
+static hipError_t launch_g(int G, const PrefillArgs& a, hipStream_t st) {
+    if constexpr (PAGED) {
+        if (a.decode_blocks > 0) return launch_gf<E, true, true>(G, a, st);
+    }
+    return launch_gf<E, PAGED, false>(G, a, st);
 }
 
 template <bool PAGED>
@@ -851,7 +873,9 @@ size_t prefill_workspace_bytes(int resident) {
     return resident > 0 ? prefill_counter_bytes(resident) + (size_t)resident * kPartSlotBytes : 0;
 }
 
-hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStream_t st) {
+int prefill_group(int n_rep) { return pick_group(n_rep); }
+
+hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, int decode_rows_max, hipStream_t st) {
     const int G = pick_group(a.n_rep);
     const int BT = 32 * (4 / G);
     a.head_groups = a.n_rep / G;
@@ -859,14 +883,20 @@ hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStr
     a.tiles_per_group = a.items_per_group;
     a.total_work = a.tiles_per_group * a.n_kv_heads * a.head_groups;
     if (num_tokens <= 0 || a.num_seqs <= 0) return hipSuccess;
+    if (a.decode_blocks > 0) {
+        if (!a.skip_decode_rows || a.dec.head_groups * G != a.n_rep) return hipErrorInvalidValue;
+        a.decode_blocks = (a.decode_blocks + 7) / 8 * 8;
+    }
     if (a.part) {
         hipError_t e = prefill_resident_workgroups(a.resident);
         if (e != hipSuccess) return e;
         // A split needs all pieces in the resident slots at once, and a call
-        // has at least ceil(num_tokens / BT) query tiles per KV head group:
-        // when those already fill the slots the call cannot split, and the
-        // kernel skips its split estimate.
-        const int64_t min_tiles = (int64_t)((num_tokens + BT - 1) / BT) * a.n_kv_heads * a.head_groups;
+        // has at least ceil(num_tokens / BT) query tiles per KV head group
+        // (not counting sequences of one token when the decode workers take
+        // them): when those already fill the slots the call cannot split, and
+        // the kernel skips its split estimate.
+        const int tile_tokens = a.skip_decode_rows ? std::max(0, num_tokens - decode_rows_max) : num_tokens;
+        const int64_t min_tiles = (int64_t)((tile_tokens + BT - 1) / BT) * a.n_kv_heads * a.head_groups;
         if (min_tiles >= a.resident) {
             a.part = nullptr;
             a.counters = nullptr;
@@ -875,7 +905,9 @@ hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, hipStr
             a.total_work = a.total_work > a.resident ? a.total_work : a.resident;
         }
     }
-    return launch_dtype<true>(dtype, G, a, st);
+    hipError_t e = launch_dtype<true>(dtype, G, a, st);
+    if (e == hipSuccess && a.decode_blocks > 0) e = launch_paged_decode_merge(dtype, a.dec, a.num_seqs, st);
+    return e;
 }
 
 hipError_t launch_dense_attention(int dtype, PrefillArgs a, hipStream_t st) {

@@ -59,10 +59,12 @@ def _load() -> ctypes.CDLL:
     ]
     lib.femto_paged_attention_gemm.restype = i
     lib.femto_paged_attention_gemm.argtypes = [
-        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, i, i64, p, p, p, sz, p,
+        i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, i, p, i, i64, p, p, p, sz, p,
     ]
     lib.femto_paged_attention_gemm_workspace_size.restype = sz
-    lib.femto_paged_attention_gemm_workspace_size.argtypes = [i, i, i, i]
+    lib.femto_paged_attention_gemm_workspace_size.argtypes = [i, i, i, i, i, i]
+    lib.femto_paged_attention_gemm_split_bytes.restype = sz
+    lib.femto_paged_attention_gemm_split_bytes.argtypes = []
     lib.femto_kv_cache_write.restype = i
     lib.femto_kv_cache_write.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i, i, p, p, i, i64, p,
@@ -137,13 +139,17 @@ def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_
     return _cached_workspace(_workspaces, device, nbytes, zero=False)
 
 
-# Key-split workspaces of the prefill kernel, one per (device, stream): the
-# kernel needs them zero-filled before the first use and leaves them so.
+# Workspaces of the prefill call, one per (device, stream): the key-split part
+# at the front must be zero-filled before the first use and is left so; the
+# decode-row part behind it needs no initialisation (a grown workspace is
+# zero-filled whole).
 _prefill_workspaces: dict = {}
 
 
-def _prefill_workspace(device: torch.device, num_seqs: int, num_tokens: int, n_heads: int, n_kv_heads: int):
-    nbytes = int(_lib.femto_paged_attention_gemm_workspace_size(num_seqs, num_tokens, n_heads, n_kv_heads))
+def _prefill_workspace(device: torch.device, num_seqs: int, num_tokens: int, max_q_len: int, n_heads: int,
+                       n_kv_heads: int, num_pages_per_seq: int):
+    nbytes = int(_lib.femto_paged_attention_gemm_workspace_size(num_seqs, num_tokens, max_q_len, n_heads,
+                                                                 n_kv_heads, num_pages_per_seq))
     return _cached_workspace(_prefill_workspaces, device, nbytes, zero=True)
 
 
@@ -223,7 +229,9 @@ def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tabl
     out = torch.empty((n_heads, num_tokens, dim), dtype=q.dtype, device=q.device)
     if num_seqs <= 0 or num_tokens == 0:
         return out
-    ws, ws_bytes = _prefill_workspace(q.device, num_seqs, num_tokens, n_heads, k_pool.size(1))
+    max_q_len = int(max_q_len)
+    ws, ws_bytes = _prefill_workspace(q.device, num_seqs, num_tokens, max_q_len, n_heads, k_pool.size(1),
+                                      kv_page_tables.size(1))
     rc = _lib.femto_paged_attention_gemm(
         dtype,
         q.data_ptr(), q.stride(0), q.stride(1),
@@ -231,7 +239,7 @@ def _paged_attention_gemm(q, k_pool, v_pool, cu_seqlens, max_q_len, kv_page_tabl
         k_pool.data_ptr(), v_pool.data_ptr(),
         k_pool.size(0), k_pool.size(1), k_pool.size(2), k_pool.size(3),
         k_pool.stride(0), k_pool.stride(1), k_pool.stride(2),
-        cu_seqlens.data_ptr(), num_seqs, num_tokens, n_heads,
+        cu_seqlens.data_ptr(), num_seqs, num_tokens, max_q_len, n_heads,
         kv_page_tables.data_ptr(), kv_page_tables.size(1), kv_page_tables.stride(0),
         kv_lens.data_ptr(), positions.data_ptr(),
         ws, ws_bytes, _stream(q.device),

@@ -89,7 +89,7 @@ def test_gemv_validation_errors(C):
 
 def test_gemm_rejects_fp32(C):
     rc = C._lib.femto_paged_attention_gemm(0, 16, 128, 128, 16, 128, 128, 16, 16, 8, 8, 16, 128, 16384, 2048, 128,
-                                           16, 2, 10, 16, 16, 4, 4, 16, 16, None, 0, None)
+                                           16, 2, 10, 5, 16, 16, 4, 4, 16, 16, None, 0, None)
     assert rc == 2
     assert "not implemented for 'Float'" in C._lib.femto_attn_last_error().decode()
 
@@ -98,11 +98,12 @@ def test_gemm_workspace_size_and_checks(C):
     # The size is one slot per resident workgroup of the current device (0
     # without a device, as here); empty calls and bad head counts need none.
     size = C._lib.femto_paged_attention_gemm_workspace_size
-    assert size(0, 16, 16, 8) == 0 and size(2, 0, 16, 8) == 0
-    assert size(8, 4096, 12, 8) == 0  # heads not a multiple of kv heads
+    assert size(0, 16, 16, 16, 8, 4) == 0 and size(2, 0, 1, 16, 8, 4) == 0
+    assert size(8, 4096, 512, 12, 8, 4) == 0  # heads not a multiple of kv heads
+    assert C._lib.femto_paged_attention_gemm_split_bytes() == 0
     # with a workspace the call sizes it against the device: without one it fails cleanly
     rc = C._lib.femto_paged_attention_gemm(2, 16, 128, 128, 16, 128, 128, 16, 16, 8, 8, 16, 128, 16384, 2048, 128,
-                                           16, 2, 10, 16, 16, 4, 4, 16, 16, 256, 64, None)
+                                           16, 2, 10, 5, 16, 16, 4, 4, 16, 16, 256, 64, None)
     assert rc != 0 and C._lib.femto_attn_last_error().decode()
 
 
