@@ -101,13 +101,82 @@ class Timer:
         return statistics.fmean(ms), statistics.median(ms), wall
 
 
-def pmc_traffic(kernel_key):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if present."""
+# Sources of the decode kernels: the committed PMC summary's traffic figure is
+# used only while these files are the ones it measured.
+DECODE_SOURCES = ("csrc/paged_decode.hip", "csrc/decode_worker.h", "csrc/common.h", "csrc/launch.h")
+
+
+def sources_sha16(rel_paths):
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in rel_paths:
+        with open(os.path.join(PKG, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def pmc_traffic(kernel_key, rel_paths):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, and where
+    the figure comes from: null when the summary is missing or measured other
+    kernel sources than the current ones."""
     path = os.path.join(PROFILES, f"{kernel_key}_pmc.json")
     if not os.path.exists(path):
-        return None
+        return None, "no committed --pmc summary"
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        rec = json.load(f)
+    want = sources_sha16(rel_paths)
+    if rec.get("sources_sha16") != want:
+        return None, f"stale: profiles/{kernel_key}_pmc.json measured sources {rec.get('sources_sha16')}, now {want}"
+    return rec.get("hbm_bytes_per_launch"), f"profiles/{kernel_key}_pmc.json (sources {want}, {rec.get('head', '?')})"
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _timed_reps(fn, sample_s, min_reps=2, max_reps=50):
+    fn()  # warm
+    times = []
+    t_end = time.perf_counter() + sample_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline_prefill(w, calls, flops, what, sample_s=12.0):
+    """The reference CPU path (per-sequence gather + SDPA) on prefill calls, in the workload dtype."""
+    import torch
+
+    from oracle import sdpa_path
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+
+    def run():
+        for q, meta in calls:
+            sdpa_path.paged_prefill(q, w.k_pool, w.v_pool, meta.raw_cu_seqlens, meta.raw_block_tables,
+                                    meta.kv_lens.tolist(), meta.positions)
+
+    t, reps = _timed_reps(run, sample_s)
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "cpu_model": cpu_model(),
+        "sample": f"{what}, {reps} reps, median {t * 1e3:.1f} ms; per-sequence block gather + torch SDPA, "
+                  f"{str(w.dtype).replace('torch.', '')}",
+    }
 
 
 def cpu_baseline_decode(w, sample_s=12.0):
@@ -135,6 +204,7 @@ def cpu_baseline_decode(w, sample_s=12.0):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
+        "cpu_model": cpu_model(),
         "sample": f"whole decode batch (64 seqs), {len(times)} reps, median {t * 1e3:.1f} ms; "
                   "per-sequence block gather + torch SDPA, bf16",
     }
@@ -179,6 +249,7 @@ def main():
         wf_ms, _, _ = timer.run(fn, K, 1, write_flush=True)
         nbytes = workloads.decode_bytes(w)
         gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        traffic, traffic_source = pmc_traffic("paged_decode_bf16_qwen3_0.6b_b64", DECODE_SOURCES)
         result = {
             "metric": "paged decode attention HBM bandwidth (bf16, Qwen3-0.6B shape, B=64, ctx U[256,4096])",
             "value": round(gbs, 2),
@@ -209,7 +280,8 @@ def main():
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4),
-                "traffic": pmc_traffic("paged_decode_bf16_qwen3_0.6b_b64"),
+                "traffic": traffic,
+                "traffic_source": traffic_source,
                 "algorithmic_bytes_per_launch": nbytes,
                 "kernel": "paged_decode_kernel<BF16,2> + paged_decode_merge_kernel<BF16> (both inside the timed region)",
             },
@@ -222,6 +294,25 @@ def main():
             result["cpu_baseline"] = cpu_baseline_decode(w)
         del w
 
+        # The reference's CPU-runnable case: fp32, 4 sequences, contexts
+        # {17, 64, 200, 511}; launch-bound (a few MB), so reported as latency.
+        w = workloads.decode_fp32_small(poison=False)
+        wd = w.to(dev)
+        q, meta = wd.gemv_call(device=dev)
+        fn = lambda: ops.paged_attention_gemv(q, wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
+                                              meta.max_kv_len)
+        mean_ms, med_ms, _ = timer.run(fn, K, W)
+        nbytes = workloads.decode_bytes(w)
+        gbs = nbytes / (mean_ms * 1e-3) / 1e9
+        extra.append({
+            "workload": "paged_decode_fp32_4seqs_ctx17-511_h16_kv8", "metric": "ms per call",
+            "value": round(mean_ms, 5), "median_ms": round(med_ms, 5),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nbytes,
+                         "note": "launch-bound: two kernel launches for a few MB"},
+        })
+        del wd, w
+
     # ---------------- prefill: 8 x 512 chunks -----------------------------
     if want("prefill"):
         w = workloads.prefill_bf16_chunked(poison=False)
@@ -233,13 +324,18 @@ def main():
         mean_ms, med_ms, _ = timer.run(fn, K, W)
         flops = workloads.prefill_flops(w.chunks, w.n_heads, w.head_dim)
         tf = flops / (mean_ms * 1e-3) / 1e12
-        extra.append({
+        rec = {
             "workload": "chunked_prefill_bf16_8x512_prefix0-2048_h16_kv8",
             "metric": "TFLOP/s (causal-exact)", "value": round(tf, 2), "ms": round(mean_ms, 5),
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops},
-        })
-        del wd, w
+        }
+        del wd
+        if not args.no_cpu_baseline:
+            qc, mc = w.gemm_call(device="cpu")
+            rec["cpu_baseline"] = cpu_baseline_prefill(w, [(qc, mc)], flops, "the whole 8 x 512 batch")
+        extra.append(rec)
+        del w
 
         # Uneven batch (fewer query tiles than resident workgroups): the key
         # split balances it; the same call without a workspace runs unsplit.
@@ -286,13 +382,23 @@ def main():
         mean_ms, med_ms, _ = timer.run(fn, steps, max(1, W // 2))
         flops = workloads.prefill_flops([(2048 * c, 2048) for c in range(16)], 32, 128)
         tf = flops / (mean_ms * 1e-3) / 1e12
-        extra.append({
+        rec = {
             "workload": "long_context_prefill_bf16_llama3_8b_32k_as_16x2048",
             "metric": "TFLOP/s (causal-exact, 16 calls)", "value": round(tf, 2), "ms": round(mean_ms, 4),
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_step": flops},
-        })
-        del wd, w, calls
+        }
+        del wd, calls
+        if not args.no_cpu_baseline:
+            # one chunk (2048 tokens after a 14336-token prefix), all 32 heads
+            c = 7
+            qc, mc = workloads.long_context_chunk(w, c, device="cpu")
+            cflops = workloads.prefill_flops([(2048 * c, 2048)], 32, 128)
+            rec["cpu_baseline"] = cpu_baseline_prefill(w, [(qc, mc)], cflops,
+                                                       "chunk 7 of 16 (2048 tokens on a 14336-token prefix)",
+                                                       sample_s=15.0)
+        extra.append(rec)
+        del w
 
         # One GPU's share of the same job under 8-way tensor parallelism (4 query
         # heads, 1 KV head): 64 query tiles per chunk for 512 resident workgroups,
@@ -347,10 +453,34 @@ def main():
         dec_bytes = workloads.decode_bytes(w, seqs=range(1, 128))
         dec_bytes_logical = workloads.decode_bytes(w, seqs=range(1, 128), unique_blocks=False)
         flops = workloads.prefill_flops([w.chunks[0]], 32, 128)
+        # Floors: the decode rows' unique bytes at 8 TB/s and the prefill chunk's
+        # FLOPs at 2.5 PFLOP/s, overlapped (max) or one after the other (sum).
+        t_hbm = dec_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
+        t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12) * 1e3
+
+        def route(ms):
+            gbs_u = dec_bytes / (ms * 1e-3) / 1e9
+            gbs_l = dec_bytes_logical / (ms * 1e-3) / 1e9
+            tf = flops / (ms * 1e-3) / 1e12
+            return {"ms": round(ms, 4),
+                    "roofline": {"bound": "hbm", "achieved": round(gbs_u, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": round(gbs_u / HBM_PEAK_GBS, 4),
+                                 "achieved_logical_GBs": round(gbs_l, 1),
+                                 "frac_logical": round(gbs_l / HBM_PEAK_GBS, 4),
+                                 "prefill_tflops": round(tf, 1), "prefill_frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
+                                 "floor_ms_overlapped": round(max(t_hbm, t_mfma), 4),
+                                 "floor_ms_serial": round(t_hbm + t_mfma, 4),
+                                 "frac_of_overlapped_floor": round(max(t_hbm, t_mfma) / ms, 4)}}
+
         extra.append({
             "workload": "mixed_bf16_qwen3_8b_1x1024on4096_plus_127_decode",
-            "ms_prefill_plus_decode": round(ms_split, 4),
-            "ms_single_gemm_call": round(ms_uni, 4),
+            "metric": "ms per step (both routes)", "value": round(ms_uni, 4), "headline_route": "single_gemm_call",
+            "routes": {
+                "single_gemm_call": {**route(ms_uni), "what": "one paged_attention_gemm over all 128 sequences "
+                                     "(the CUSTOM_GEMM route); decode rows on decode wave workers in the tiles' launch"},
+                "prefill_plus_decode": {**route(ms_split), "what": "paged_attention_gemm on sequence 0, then "
+                                        "paged_attention_gemv on sequences 1-127 (the default routed engine)"},
+            },
             "prefill_flops": flops, "decode_unique_bytes": dec_bytes, "decode_logical_bytes": dec_bytes_logical,
         })
         del wd, w
