@@ -83,6 +83,13 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // base and lds_base must be the same in every lane of the wave.  m0 is on the
 // clobber list; clang warns that it is reserved, but nothing else in these
 // kernels uses m0 (their assembly sets it only here), so the warning is muted.
+//
+// The compiler inserts no hazard wait states inside inline asm, so the block
+// carries the two that gfx9 requires here: a VMEM instruction may read an
+// SGPR only 5 wait states after a VALU instruction wrote it (the base and the
+// m0 value usually come straight from v_readfirstlane), and an LDS DMA may
+// read m0 only 1 wait state after an SALU instruction wrote it.  Without them
+// a copy can use a stale base register and read from a wrong address.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds_base) {
@@ -92,7 +99,9 @@ __device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint3
     const uint64_t sb = ((uint64_t)hi << 32) | lo;
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
     asm volatile(
+        "s_nop 4\n\t"
         "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
         "global_load_lds_dwordx4 %0, %1"
         :
         : "v"(voff), "s"(sb), "s"(m0v)

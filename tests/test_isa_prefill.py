@@ -80,3 +80,22 @@ def test_no_wait_between_tile_copies(tmp_path):
                 bad.append((name, bname, waits))
     assert blocks_with_copies >= 18
     assert not bad, f"vmcnt waits between direct-to-LDS copies: {bad[:4]}"
+
+
+def test_copies_carry_hazard_wait_states(tmp_path):
+    """Each direct-to-LDS copy is issued from inline asm, where the compiler
+    inserts no hazard wait states: the asm must provide the 5 wait states
+    between a VALU write of an SGPR (v_readfirstlane of the base and of the
+    m0 value) and the VMEM instruction that reads it, and the 1 between the
+    m0 write and the LDS DMA.  Without them a copy can read a stale base
+    register and fetch from a wrong address."""
+    asm = _compile_to_asm(tmp_path)
+    n = 0
+    for name, body in _kernels(asm):
+        ins = [t for _, block in _blocks(body) for t in block]
+        for k, t in enumerate(ins):
+            if t.startswith("global_load_lds_dwordx4"):
+                n += 1
+                assert ins[k - 1].startswith("s_nop 0") and ins[k - 2].startswith("s_mov_b32 m0") \
+                    and ins[k - 3].startswith("s_nop 4"), (name, ins[max(0, k - 4):k + 1])
+    assert n >= 18 * 8
