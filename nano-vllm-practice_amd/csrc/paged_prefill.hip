@@ -161,6 +161,20 @@ __device__ __forceinline__ int block_incl_scan(int v, int* s_red, int& total) {
     return v + off;
 }
 
+// Position in an XCD's stretch of the work list of the k-th workgroup the
+// XCD receives: the first `cus` workgroups take one slot on each of its CUs,
+// the next `cus` the second slot, and so on.  Every other round is dealt in
+// reverse, so a CU whose first item is one of the heaviest of the stretch
+// (a sequence's items come heaviest first) gets one of the lightest as its
+// second; the heavy item then runs alone once the light one is done.
+__device__ __forceinline__ int serpentine(int k, int n, int cus) {
+    if (cus <= 0) return k;
+    const int round = k / cus, pos = k - round * cus;
+    if ((round & 1) == 0) return k;
+    const int in_round = min(cus, n - round * cus);
+    return round * cus + (in_round - 1 - pos);
+}
+
 template <typename E, int G, bool PAGED, bool FUSED>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_mfma_kernel(PrefillArgs a) {
     constexpr int EB = 2;
@@ -259,7 +273,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int work = groups * total;
             const int per_xcd = (work + 7) >> 3;
             if ((lin >> 3) >= per_xcd) return;
-            w = (lin & 7) * per_xcd + (lin >> 3);
+            w = (lin & 7) * per_xcd + serpentine(lin >> 3, per_xcd, a.resident >> 4);
             if (w >= work) return;
             grp = w / total;
             tile_lin = w - grp * total;
@@ -310,7 +324,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             const int work = groups * total;
             const int per_xcd = (work + 7) >> 3;
             if ((lin >> 3) >= per_xcd) return;
-            w = (lin & 7) * per_xcd + (lin >> 3);
+            w = (lin & 7) * per_xcd + (split ? (lin >> 3) : serpentine(lin >> 3, per_xcd, a.resident >> 4));
             if (w >= work) return;
             grp = w / total;
             tile_lin = w - grp * total;
@@ -892,6 +906,10 @@ hipError_t launch_paged_prefill(int dtype, PrefillArgs a, int num_tokens, int de
     a.tiles_per_group = a.items_per_group;
     a.total_work = a.tiles_per_group * a.n_kv_heads * a.head_groups;
     if (num_tokens <= 0 || a.num_seqs <= 0) return hipSuccess;
+    {
+        hipError_t e = prefill_resident_workgroups(a.resident);
+        if (e != hipSuccess) return e;
+    }
     if (a.decode_blocks > 0) {
         if (!a.skip_decode_rows || a.dec.head_groups * G != a.n_rep) return hipErrorInvalidValue;
         a.decode_blocks = (a.decode_blocks + 7) / 8 * 8;
