@@ -92,20 +92,52 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 // a copy can use a stale base register and read from a wrong address.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const void* base, uint32_t voff, uint32_t lds_base) {
+__device__ __forceinline__ uint64_t wave_base(const void* base) {
     const uint64_t b = (uint64_t)(uintptr_t)base;
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-    const uint64_t sb = ((uint64_t)hi << 32) | lo;
-    const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// One page of K and one of V: four copies of each, the copy j of K landing
+// at kd + 1024 j and of V at vd + 1024 j.  All eight go out from one asm
+// block, so the 5 wait states after the SGPR writes are paid once; each m0
+// step (an SALU write) is followed by the 1 wait state the DMA needs.
+__device__ __forceinline__ void lds_dma_page(const void* kbase, const void* vbase, const uint32_t (&ko)[4],
+                                             const uint32_t (&vo)[4], uint32_t kd, uint32_t vd) {
+    const uint64_t kb = wave_base(kbase), vb = wave_base(vbase);
+    const uint32_t km0 = __builtin_amdgcn_readfirstlane(kd);
+    const uint32_t vm0 = __builtin_amdgcn_readfirstlane(vd);
     asm volatile(
         "s_nop 4\n\t"
-        "s_mov_b32 m0, %2\n\t"
+        "s_mov_b32 m0, %10\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %0, %1"
+        "global_load_lds_dwordx4 %0, %8\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %8\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, %8\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %3, %8\n\t"
+        "s_mov_b32 m0, %11\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %4, %9\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %5, %9\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %6, %9\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %7, %9"
         :
-        : "v"(voff), "s"(sb), "s"(m0v)
-        : "memory", "m0");
+        : "v"(ko[0]), "v"(ko[1]), "v"(ko[2]), "v"(ko[3]), "v"(vo[0]), "v"(vo[1]), "v"(vo[2]), "v"(vo[3]),
+          "s"(kb), "s"(vb), "s"(km0), "s"(vm0)
+        : "memory", "m0", "scc");
 }
 #pragma clang diagnostic pop
 
@@ -409,14 +441,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // copies of a full tile use the precomputed page offsets, so the issue
     // path does no address arithmetic that could tie it to a pending load.
     const int rs_k = (int)a.k_stride2 * EB, rs_v = (int)a.v_stride2 * EB;
-    int koff[4], voff[4], kfull[4], vfull[4];
+    int koff[4], voff[4];
+    uint32_t kfull[4], vfull[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = 4 * j + lrow;
         koff[j] = ((lpos ^ swz_k(r)) << 4);
         voff[j] = ((lpos ^ swz_v(r)) << 4);
-        kfull[j] = r * rs_k + koff[j];
-        vfull[j] = r * rs_v + voff[j];
+        kfull[j] = (uint32_t)(r * rs_k + koff[j]);
+        vfull[j] = (uint32_t)(r * rs_v + voff[j]);
     }
     // Block ids for this wave's page of tiles tbase .. tbase+63, one per lane.
     int tbl = -1, tbase = 0;
@@ -457,20 +490,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint32_t kd = lds_addr(&smem[stage][0][(16 * wave) * kRowBytes]);
         const uint32_t vd = lds_addr(&smem[stage][1][(16 * wave) * kRowBytes]);
         if (ok && last_row >= kPage - 1) {  // a full page of the pool (wave-uniform)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lds_dma16(kp, (uint32_t)kfull[j], kd + j * 1024);
-                lds_dma16(vp, (uint32_t)vfull[j], vd + j * 1024);
-            }
+            lds_dma_page(kp, vp, kfull, vfull, kd, vd);
         } else {
             // The sequence's last page (rows past kv_len repeat its last row)
             // or the zero page (every row reads row 0: all of it is zeros).
+            uint32_t ko[4], vo[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = ok ? min(4 * j + lrow, last_row) : 0;
-                lds_dma16(kp, (uint32_t)(row * rs_k + koff[j]), kd + j * 1024);
-                lds_dma16(vp, (uint32_t)(row * rs_v + voff[j]), vd + j * 1024);
+                ko[j] = (uint32_t)(row * rs_k + koff[j]);
+                vo[j] = (uint32_t)(row * rs_v + voff[j]);
             }
+            lds_dma_page(kp, vp, ko, vo, kd, vd);
         }
     };
 

@@ -86,16 +86,29 @@ def test_copies_carry_hazard_wait_states(tmp_path):
     """Each direct-to-LDS copy is issued from inline asm, where the compiler
     inserts no hazard wait states: the asm must provide the 5 wait states
     between a VALU write of an SGPR (v_readfirstlane of the base and of the
-    m0 value) and the VMEM instruction that reads it, and the 1 between the
+    m0 value) and the VMEM instruction that reads it, and the 1 between an
     m0 write and the LDS DMA.  Without them a copy can read a stale base
-    register and fetch from a wrong address."""
+    register and fetch from a wrong address.  A page's eight copies form one
+    run: s_nop 4, then per copy an m0 write, s_nop 0 and the copy."""
     asm = _compile_to_asm(tmp_path)
     n = 0
     for name, body in _kernels(asm):
         ins = [t for _, block in _blocks(body) for t in block]
-        for k, t in enumerate(ins):
-            if t.startswith("global_load_lds_dwordx4"):
-                n += 1
-                assert ins[k - 1].startswith("s_nop 0") and ins[k - 2].startswith("s_mov_b32 m0") \
-                    and ins[k - 3].startswith("s_nop 4"), (name, ins[max(0, k - 4):k + 1])
-    assert n >= 18 * 8
+        k = 0
+        while k < len(ins):
+            if not ins[k].startswith("s_nop 4"):
+                k += 1
+                continue
+            run, j = 0, k + 1
+            while j + 2 < len(ins) and re.match(r"s_(mov_b32|add_u32) m0,", ins[j]) \
+                    and ins[j + 1].startswith("s_nop 0") and ins[j + 2].startswith("global_load_lds_dwordx4"):
+                run += 1
+                j += 3
+            if run:
+                assert run == 8, (name, ins[k:j + 1])
+                n += run
+            k = max(j, k + 1)
+    total = sum(t.startswith("global_load_lds_dwordx4") for _, body in _kernels(asm)
+                for _, block in _blocks(body) for t in block)
+    # every copy sits in such a run
+    assert n == total and n >= 18 * 8, (n, total)
