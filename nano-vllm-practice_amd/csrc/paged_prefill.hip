@@ -587,17 +587,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint8_t* vs = smem[STAGE][1];
 
         // S^T blocks: keys kb + 32*kb2 + (0..31), queries = lanes (raw scores).
-        f32x16 sacc[2];
+        // The two blocks' MFMA chains alternate, and the K fragments of step
+        // kk are read at step kk - 2, so an MFMA does not wait out a full LDS
+        // read latency (with one chain after the other and one fragment
+        // register, every MFMA of the first chain did).
+        f32x16 sacc[2] = {f32x16{}, f32x16{}};
+        auto kfrag = [&](int kk, int kb2) {
+            const int chunk = (2 * kk + h2) ^ k_sw;
+            return *reinterpret_cast<const u32x4*>(ks + k_rd + kb2 * 32 * kRowBytes + (chunk << 4));
+        };
+        u32x4 kf[3][2];
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-            sacc[kb2] = f32x16{};
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const int chunk = (2 * kk + h2) ^ k_sw;
-                const u32x4 ka = *reinterpret_cast<const u32x4*>(ks + k_rd + kb2 * 32 * kRowBytes + (chunk << 4));
-                sacc[kb2] = mfma32x32x16(E{}, ka, qreg[kk], sacc[kb2]);
-            }
+        for (int kk = 0; kk < 2; ++kk) {
+            kf[kk][0] = kfrag(kk, 0);
+            kf[kk][1] = kfrag(kk, 1);
         }
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            if (kk + 2 < 8) {
+                kf[(kk + 2) % 3][0] = kfrag(kk + 2, 0);
+                kf[(kk + 2) % 3][1] = kfrag(kk + 2, 1);
+            }
+            sacc[0] = mfma32x32x16(E{}, kf[kk % 3][0], qreg[kk], sacc[0]);
+            sacc[1] = mfma32x32x16(E{}, kf[kk % 3][1], qreg[kk], sacc[1]);
+        }
+        // Keep that order: 4 reads, then 6 x (2 reads, 2 MFMAs), then 4 MFMAs.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int g = 0; g < 6; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         // Accumulator i of block kb2 holds key kb + 32*kb2 + 8*(i/4) + 4*h2 + i%4.
         float mx = -INFINITY;
         if (kb + kKvTile > kfull_w) {  // wave-uniform: tile crosses some row's limit
