@@ -227,7 +227,13 @@ def test_many_sequences_with_one_split(ops, gpu, monkeypatch):
 def test_tp8_share_long_chunk(ops, gpu, monkeypatch):
     """One GPU's share under 8-way tensor parallelism (4 query heads, 1 KV
     head): a 2048-token chunk after a 6144-token prefix has 64 query tiles for
-    the whole GPU, and each is split into 8 pieces."""
+    the whole GPU, and each is split into 8 pieces.
+
+    The handoff crosses XCDs on every tile: the work list is piece-major
+    (piece p of query tile i is item i + 64 p) and each XCD (workgroup id
+    mod 8) takes a contiguous eighth of the 512 items, so the 8 pieces of a
+    tile run on 8 different XCDs and the merging piece reads partials that
+    the other 7 wrote through their own L2s."""
     chunks = [(6144, 2048)]
     assert split_plan(chunks, 4, 1, _cus()) == [8]
     w = workloads.make_paged_workload("tp8", chunks, 4, 1, seed=1004)
