@@ -171,6 +171,7 @@ def cpu_baseline_prefill(w, calls, flops, what, sample_s=12.0):
     return {
         "value": round(flops / t / 1e12, 4),
         "unit": "TFLOP/s",
+        "median_ms": round(t * 1e3, 2),
         "cores": threads,
         "kind": "port",
         "cpu_model": cpu_model(),
@@ -433,57 +434,80 @@ def main():
 
     # ---------------- unified mixed batch ---------------------------------
     if want("mixed"):
+        def mixed_entry(w, name, cpu):
+            """Both routes of a unified batch: sequence 0 a prefill chunk, the rest decode rows."""
+            n = len(w.chunks)
+            wd = w.to(dev)
+            qp, mp = wd.gemm_call(seqs=[0], device=dev)
+            qd, md = wd.gemv_call(seqs=range(1, n), device=dev)
+            qa, ma = wd.gemm_call(device=dev)
+
+            def route_split():
+                ops.paged_attention_gemm(qp, wd.k_pool, wd.v_pool, mp.cu_seqlens, mp.max_q_len, mp.Q_TILE_SIZE,
+                                         mp.cu_q_tiles, mp.q_tile_to_seq_idx, mp.block_tables, mp.kv_lens,
+                                         mp.positions)
+                ops.paged_attention_gemv(qd, wd.k_pool, wd.v_pool, md.block_tables, md.kv_lens, md.max_kv_len)
+
+            def route_unified():
+                ops.paged_attention_gemm(qa, wd.k_pool, wd.v_pool, ma.cu_seqlens, ma.max_q_len, ma.Q_TILE_SIZE,
+                                         ma.cu_q_tiles, ma.q_tile_to_seq_idx, ma.block_tables, ma.kv_lens,
+                                         ma.positions)
+
+            ms_split, _, _ = timer.run(route_split, K, W)
+            ms_uni, _, _ = timer.run(route_unified, K, W)
+            dec_bytes = workloads.decode_bytes(w, seqs=range(1, n))
+            dec_bytes_logical = workloads.decode_bytes(w, seqs=range(1, n), unique_blocks=False)
+            flops = workloads.prefill_flops([w.chunks[0]], w.n_heads, w.head_dim)
+            # Floors: the decode rows' unique bytes at 8 TB/s and the prefill
+            # chunk's FLOPs at 2.5 PFLOP/s, overlapped (max) or one after the
+            # other (sum).
+            t_hbm = dec_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
+            t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12) * 1e3
+
+            def route(ms):
+                gbs_u = dec_bytes / (ms * 1e-3) / 1e9
+                gbs_l = dec_bytes_logical / (ms * 1e-3) / 1e9
+                tf = flops / (ms * 1e-3) / 1e12
+                return {"ms": round(ms, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs_u, 1), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs_u / HBM_PEAK_GBS, 4),
+                                     "achieved_logical_GBs": round(gbs_l, 1),
+                                     "frac_logical": round(gbs_l / HBM_PEAK_GBS, 4),
+                                     "prefill_tflops": round(tf, 1),
+                                     "prefill_frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
+                                     "floor_ms_overlapped": round(max(t_hbm, t_mfma), 4),
+                                     "floor_ms_serial": round(t_hbm + t_mfma, 4),
+                                     "frac_of_overlapped_floor": round(max(t_hbm, t_mfma) / ms, 4)}}
+
+            rec = {
+                "workload": name,
+                "metric": "ms per step (both routes)", "value": round(ms_uni, 4),
+                "headline_route": "single_gemm_call" if ms_uni <= ms_split else "prefill_plus_decode",
+                "routes": {
+                    "single_gemm_call": {**route(ms_uni), "what": f"one paged_attention_gemm over all {n} sequences "
+                                         "(the CUSTOM_GEMM route); decode rows on decode wave workers"},
+                    "prefill_plus_decode": {**route(ms_split), "what": "paged_attention_gemm on sequence 0, then "
+                                            f"paged_attention_gemv on sequences 1-{n - 1} (the default routed engine)"},
+                },
+                "prefill_flops": flops, "decode_unique_bytes": dec_bytes, "decode_logical_bytes": dec_bytes_logical,
+            }
+            del wd
+            if cpu and not args.no_cpu_baseline:
+                qc, mc = w.gemm_call(device="cpu")
+                cb = cpu_baseline_prefill(w, [(qc, mc)], flops, f"the whole {n}-sequence batch in one call")
+                t_cpu = cb["median_ms"] * 1e-3
+                rec["cpu_baseline"] = {**cb, "value": cb["median_ms"], "unit": "ms per step",
+                                       "prefill_tflops": cb["value"],
+                                       "decode_unique_GBs": round(dec_bytes / t_cpu / 1e9, 3)}
+            return rec
+
         w = workloads.mixed_bf16_qwen3_8b(poison=False)
-        wd = w.to(dev)
-        qp, mp = wd.gemm_call(seqs=[0], device=dev)
-        qd, md = wd.gemv_call(seqs=range(1, 128), device=dev)
-        qa, ma = wd.gemm_call(device=dev)
-
-        def route_split():
-            ops.paged_attention_gemm(qp, wd.k_pool, wd.v_pool, mp.cu_seqlens, mp.max_q_len, mp.Q_TILE_SIZE,
-                                     mp.cu_q_tiles, mp.q_tile_to_seq_idx, mp.block_tables, mp.kv_lens, mp.positions)
-            ops.paged_attention_gemv(qd, wd.k_pool, wd.v_pool, md.block_tables, md.kv_lens, md.max_kv_len)
-
-        def route_unified():
-            ops.paged_attention_gemm(qa, wd.k_pool, wd.v_pool, ma.cu_seqlens, ma.max_q_len, ma.Q_TILE_SIZE,
-                                     ma.cu_q_tiles, ma.q_tile_to_seq_idx, ma.block_tables, ma.kv_lens, ma.positions)
-
-        ms_split, _, _ = timer.run(route_split, K, W)
-        ms_uni, _, _ = timer.run(route_unified, K, W)
-        dec_bytes = workloads.decode_bytes(w, seqs=range(1, 128))
-        dec_bytes_logical = workloads.decode_bytes(w, seqs=range(1, 128), unique_blocks=False)
-        flops = workloads.prefill_flops([w.chunks[0]], 32, 128)
-        # Floors: the decode rows' unique bytes at 8 TB/s and the prefill chunk's
-        # FLOPs at 2.5 PFLOP/s, overlapped (max) or one after the other (sum).
-        t_hbm = dec_bytes / (HBM_PEAK_GBS * 1e9) * 1e3
-        t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12) * 1e3
-
-        def route(ms):
-            gbs_u = dec_bytes / (ms * 1e-3) / 1e9
-            gbs_l = dec_bytes_logical / (ms * 1e-3) / 1e9
-            tf = flops / (ms * 1e-3) / 1e12
-            return {"ms": round(ms, 4),
-                    "roofline": {"bound": "hbm", "achieved": round(gbs_u, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                 "frac": round(gbs_u / HBM_PEAK_GBS, 4),
-                                 "achieved_logical_GBs": round(gbs_l, 1),
-                                 "frac_logical": round(gbs_l / HBM_PEAK_GBS, 4),
-                                 "prefill_tflops": round(tf, 1), "prefill_frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4),
-                                 "floor_ms_overlapped": round(max(t_hbm, t_mfma), 4),
-                                 "floor_ms_serial": round(t_hbm + t_mfma, 4),
-                                 "frac_of_overlapped_floor": round(max(t_hbm, t_mfma) / ms, 4)}}
-
-        extra.append({
-            "workload": "mixed_bf16_qwen3_8b_1x1024on4096_plus_127_decode",
-            "metric": "ms per step (both routes)", "value": round(ms_uni, 4), "headline_route": "single_gemm_call",
-            "routes": {
-                "single_gemm_call": {**route(ms_uni), "what": "one paged_attention_gemm over all 128 sequences "
-                                     "(the CUSTOM_GEMM route); decode rows on decode wave workers in the tiles' launch"},
-                "prefill_plus_decode": {**route(ms_split), "what": "paged_attention_gemm on sequence 0, then "
-                                        "paged_attention_gemv on sequences 1-127 (the default routed engine)"},
-            },
-            "prefill_flops": flops, "decode_unique_bytes": dec_bytes, "decode_logical_bytes": dec_bytes_logical,
-        })
-        del wd, w
+        extra.append(mixed_entry(w, "mixed_bf16_qwen3_8b_1x1024on4096_plus_127_decode", cpu=True))
+        del w
+        # One GPU's share of the same batch under 8-way tensor parallelism.
+        w = workloads.mixed_bf16_qwen3_8b_tp8_share(poison=False)
+        extra.append(mixed_entry(w, "mixed_bf16_qwen3_8b_tp8_share_h4_kv1", cpu=False))
+        del w
 
     # ---------------- dense flash attention (reference benchmark shapes) --
     if want("flash"):

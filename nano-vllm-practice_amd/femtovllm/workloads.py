@@ -283,6 +283,19 @@ def mixed_bf16_qwen3_8b(poison=True) -> PagedWorkload:
     )
 
 
+def mixed_bf16_qwen3_8b_tp8_share(poison=True) -> PagedWorkload:
+    """One GPU's share of the unified batch under 8-way tensor parallelism
+    (Qwen3-8B shape split by KV head): 4 query heads and 1 KV head, the same
+    sequences, context lengths and shared prefix blocks as ``mixed_bf16_qwen3_8b``."""
+    rng = np.random.default_rng(1005)
+    lens = [int(x) for x in rng.integers(512, 8192, size=127, endpoint=True)]
+    chunks = [(4096, 1024)] + [(L - 1, 1) for L in lens]
+    return make_paged_workload(
+        "mixed_bf16_qwen3_8b_tp8", chunks, 4, 1, seed=1005, poison=poison, rng=rng,
+        shared_seqs=tuple(range(0, 128, 2)), shared_blocks=64,
+    )
+
+
 def reference_fixture(dtype=torch.bfloat16) -> PagedWorkload:
     """The structure of the reference's paged prefill test.
 

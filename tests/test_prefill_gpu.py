@@ -227,3 +227,28 @@ def test_strided_q_and_errors(ops, gpu):
     with pytest.raises(RuntimeError):
         qf = q.float().to(gpu)
         run_gemm(ops, qf, meta, wd.k_pool.float(), wd.v_pool.float(), gpu)
+
+
+def test_mixed_batch_tp8_share_both_routes(ops, gpu):
+    """One GPU's share of the unified batch under 8-way tensor parallelism
+    (4 query heads, 1 KV head): the single call and the prefill + decode
+    route, every decode row and sampled rows of the 1024-token chunk."""
+    w = workloads.mixed_bf16_qwen3_8b_tp8_share()
+    q, meta = w.gemm_call()
+    cu = meta.raw_cu_seqlens
+    rows = sorted(set(sample_rows(cu[:2], 48, np.random.default_rng(3))) | set(range(1024, cu[-1])))
+    want = oa.paged_prefill(np64(q), np32(w.k_pool), np32(w.v_pool), cu, np_tables(meta), meta.kv_lens.tolist(),
+                            np.asarray(meta.raw_positions), rows=rows)
+    mask = np.zeros(want.shape, dtype=bool)
+    mask[:, rows] = True
+    wd = w.to(gpu)
+    qg, mg = w.gemm_call(device=gpu)
+    out = run_gemm(ops, qg, mg, wd.k_pool, wd.v_pool, gpu)
+    assert_close(out, want, torch.bfloat16, "tp8 share mixed batch, one call", mask=mask)
+    qp, mp = w.gemm_call(seqs=[0], device=gpu)
+    outp = run_gemm(ops, qp, mp, wd.k_pool, wd.v_pool, gpu)
+    qd, md = w.gemv_call(seqs=range(1, 128), device=gpu)
+    outd = ops.paged_attention_gemv(qd.to(gpu), wd.k_pool, wd.v_pool, md.block_tables, md.kv_lens, md.max_kv_len)
+    torch.cuda.synchronize()
+    assert_close(torch.cat([outp, outd], dim=1), want, torch.bfloat16, "tp8 share mixed batch, two calls",
+                 mask=mask)
