@@ -112,8 +112,9 @@ int femto_paged_attention_gemv_noalloc(
  * takes it; it only bounds how many sequences may have exactly one token.
  * workspace may be NULL.  With a workspace of at least
  * femto_paged_attention_gemm_workspace_size() bytes (256-byte aligned; its
- * first femto_paged_attention_gemm_split_bytes() bytes zero-filled before
- * the first use, and every call leaves them zero-filled):
+ * first femto_paged_attention_gemm_split_bytes() bytes, the key-split
+ * counters, zero-filled before the first use, and every call leaves them
+ * zero-filled):
  *  - the query tiles of sequences much longer than the average are split
  *    over their keys and merged within the launch, so a few long sequences
  *    do not set the length of the call;
@@ -150,8 +151,9 @@ size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, i
                                                  int n_kv_heads, int num_pages_per_seq);
 
 /* Leading bytes of that workspace that must be zero-filled before its first
- * use (the key-split counters and partial slots; the decode-row part needs no
- * initialisation).  No counterpart in the reference. */
+ * use: the key-split counters (the partial slots behind them and the
+ * decode-row part need no initialisation).  No counterpart in the
+ * reference. */
 size_t femto_paged_attention_gemm_split_bytes(void);
 
 /* KV-cache write: scatter new K/V rows into the paged pools, bit-exact.

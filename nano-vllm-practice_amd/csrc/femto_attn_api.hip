@@ -285,7 +285,7 @@ size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, i
 size_t femto_paged_attention_gemm_split_bytes(void) {
     int resident = 0;
     if (femto::prefill_resident_workgroups(resident) != hipSuccess) return 0;
-    return femto::prefill_workspace_bytes(resident);
+    return femto::prefill_counter_bytes(resident);
 }
 
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len) {

@@ -42,7 +42,8 @@
 //    system-scope loads, merges them into its registers and writes the
 //    output.  Only the partials bypass the caches, so no cache-wide
 //    write-back or invalidate is needed.  The last piece also resets the
-//    counter and clears the slots, leaving the workspace all zeros.
+//    counter, leaving the counters all zero; a slot is always written in
+//    the call that reads it, so the slots need no clearing.
 #include <algorithm>
 #include <type_traits>
 
@@ -855,15 +856,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                     }
                 }
             }
-        }
-        // Every partial was consumed (the merged values depend on them):
-        // clear the slots for later calls.
-        for (int p = 0; p < nne; ++p) {
-            uint8_t* sp = slot_of(p);
-#pragma unroll
-            for (int k = 0; k < kLoads; ++k) *reinterpret_cast<f32x4*>(sp + lane_acc + k * 1024) = f32x4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (kHalf) *reinterpret_cast<uint32_t*>(sp + 32768 + (wave * 64 + lane) * 4) = 0u;
-            *reinterpret_cast<u32x2*>(sp + lane_ml) = u32x2{0u, 0u};
         }
     }
 

@@ -139,10 +139,10 @@ def _decode_workspace(device: torch.device, num_seqs: int, n_heads: int, max_kv_
     return _cached_workspace(_workspaces, device, nbytes, zero=False)
 
 
-# Workspaces of the prefill call, one per (device, stream): the key-split part
-# at the front must be zero-filled before the first use and is left so; the
-# decode-row part behind it needs no initialisation (a grown workspace is
-# zero-filled whole).
+# Workspaces of the prefill call, one per (device, stream): the key-split
+# counters at the front must be zero-filled before the first use and are left
+# so; the partial slots and the decode-row part behind them need no
+# initialisation (a grown workspace is zero-filled whole).
 _prefill_workspaces: dict = {}
 
 

@@ -5,7 +5,7 @@ sequences much longer than the average work per resident workgroup into up
 to eight pieces over their keys; the last piece to finish merges the others'
 partial softmax states within the launch.  The results must match the oracle
 (the reference's attention, paged_attention_gemm.py:83-160) and the unsplit
-kernel, and every call must leave the workspace zero-filled.
+kernel, and every call must leave the split counters zero-filled.
 """
 
 import dataclasses
@@ -38,9 +38,9 @@ def _unsplit(ops, q, meta, wd, monkeypatch):
 
 
 def _workspace_is_zero(device):
-    """The key-split part of every cached workspace (its first
+    """The key-split counters of every cached workspace (its first
     femto_paged_attention_gemm_split_bytes() bytes from the 256-byte aligned
-    start) is back to zeros."""
+    start) are back to zeros."""
     from femtovllm import _C
 
     split = int(_C._lib.femto_paged_attention_gemm_split_bytes())
@@ -86,7 +86,7 @@ def _check(ops, w, gpu, monkeypatch, rows_per_seq=6, what=""):
     q = q.to(gpu)
     wd = w.to(gpu)
     out = _gemm(ops, q, meta, wd)
-    assert _workspace_is_zero(gpu), f"workspace not cleared after {what}"
+    assert _workspace_is_zero(gpu), f"split counters not reset after {what}"
     cu = meta.raw_cu_seqlens
     # sequences of one token run on the decode kernel (its own rounding), so
     # they are checked against the oracle, every one, and not against the
@@ -114,6 +114,30 @@ def test_long_sequence_among_short(ops, gpu, monkeypatch, long_prefix, pieces):
     w = workloads.make_paged_workload(f"split{long_prefix}", chunks, 16, 8, seed=long_prefix)
     err = _check(ops, w, gpu, monkeypatch, what=f"long prefix {long_prefix}")
     print(f"long prefix {long_prefix}: {pieces} pieces, max abs err {err:.2e}")
+
+
+def test_partial_slots_need_no_zeros(ops, gpu, monkeypatch):
+    """Only the counters must start at zero: every partial slot a merge reads
+    was written in the same call.  With everything behind the counters (the
+    partial slots) filled with 0xff bytes, NaN in every float, a call split
+    into 8 pieces per long query tile still matches the oracle."""
+    from femtovllm import _C
+
+    chunks = [(6000, 192)] + [(int(p), 64) for p in np.linspace(0, 300, 40)]
+    assert split_plan(chunks, 16, 8, _cus())[0] == 8
+    w = workloads.make_paged_workload("dirty_slots", chunks, 16, 8, seed=6000)
+    q, meta = w.gemm_call(device=gpu)
+    _gemm(ops, q.to(gpu), meta, w.to(gpu))  # the cached workspace exists from here on
+    counters = int(_C._lib.femto_paged_attention_gemm_split_bytes())
+    filled = 0
+    for key, ws in _C._prefill_workspaces.items():
+        if key[0] == gpu.index:
+            off = (-ws.data_ptr()) % 256
+            ws[off + counters:].fill_(0xFF)
+            filled += 1
+    torch.cuda.synchronize()
+    assert filled
+    _check(ops, w, gpu, monkeypatch, what="partial slots full of 0xff bytes")
 
 
 def test_fresh_prompt_is_split_by_causal_length(ops, gpu, monkeypatch):
