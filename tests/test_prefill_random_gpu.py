@@ -1,0 +1,88 @@
+"""Seeded random batches through the HIP prefill kernel, checked against the oracle.
+
+Each case draws a batch the hand-written cases may not reach: 1-10
+sequences whose chunks are empty, one token (decode rows), short or a few
+hundred tokens, after no, short or long cached prefixes, with a random head
+layout and storage type.  One call covers the query-tile mapping, the key
+split of long tiles (whenever a sequence's keys far exceed the mean work per
+resident workgroup), and the decode rows, fused into the launch or run
+before it by head ratio.  Each call must match the oracle (the reference's
+attention, femtovllm/ops/triton/paged_attention/paged_attention_gemm.py:83-160)
+and the call without key split, and leave the split counters zero-filled.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as oa
+from femtovllm import workloads
+from helpers import assert_close, np32, np64, np_tables, sample_rows
+from test_prefill_split_gpu import _gemm, _unsplit, _workspace_is_zero, split_plan
+
+HEADS = [(8, 8), (16, 8), (32, 8), (64, 8), (12, 4), (28, 4), (40, 8), (8, 1), (4, 1), (6, 2), (3, 3)]
+# Oracle work allowed per case (rows x keys x query heads) before rows are sampled.
+FULL_CHECK = 2e8
+
+
+def random_batch(seed):
+    rng = np.random.default_rng(seed)
+    H, KVH = HEADS[int(rng.integers(len(HEADS)))]
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    chunks = []
+    for _ in range(int(rng.integers(1, 11))):
+        r = rng.random()
+        prefix = 0 if r < 0.3 else int(rng.integers(1, 200)) if r < 0.7 else int(rng.integers(200, 4000))
+        r = rng.random()
+        n = 0 if r < 0.1 else 1 if r < 0.3 else int(rng.integers(2, 64)) if r < 0.7 else int(rng.integers(64, 400))
+        chunks.append((prefix, n))
+    if all(n == 0 for _, n in chunks):
+        chunks[0] = (chunks[0][0], 1)
+    return chunks, H, KVH, dtype
+
+
+def test_generator_reaches_every_kind_of_sequence():
+    """Over the seeds used below: empty chunks, one-token rows, long prefixes,
+    fresh prompts and both storage types all occur, and on a 256-CU GPU most
+    calls cut some query tiles into key pieces."""
+    seen = set()
+    split = 0
+    for seed in range(64):
+        chunks, H, KVH, dtype = random_batch(7000 + seed)
+        split += max(split_plan(chunks, H, KVH, 256)) > 1
+        seen.add(dtype)
+        for p, n in chunks:
+            seen.add("empty" if n == 0 else "one" if n == 1 else "chunk")
+            seen.add("fresh" if p == 0 else "long" if p >= 200 else "short")
+    assert seen >= {torch.bfloat16, torch.float16, "empty", "one", "chunk", "fresh", "long", "short"}
+    assert split >= 32
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(64))
+def test_random_batch(ops, gpu, monkeypatch, seed):
+    chunks, H, KVH, dtype = random_batch(7000 + seed)
+    what = f"seed {7000 + seed}: H={H} KVH={KVH} {dtype} chunks {chunks}"
+    print(what, flush=True)
+    w = workloads.make_paged_workload("random", chunks, H, KVH, dtype=dtype, seed=7000 + seed)
+    q, meta = w.gemm_call(device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    out = _gemm(ops, q, meta, wd)
+    assert _workspace_is_zero(gpu), f"split counters not reset after {what}"
+    cu = meta.raw_cu_seqlens
+    work = sum((cu[b + 1] - cu[b]) * (p + n) for b, (p, n) in enumerate(chunks)) * H
+    rows = None
+    if work > FULL_CHECK:
+        rows = sorted(set(sample_rows(cu, 12, np.random.default_rng(seed))))
+    want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), cu, np_tables(meta),
+                            meta.kv_lens.tolist(), np.asarray(meta.raw_positions), rows=rows)
+    mask = None
+    if rows is not None:
+        mask = np.zeros(want.shape, dtype=bool)
+        mask[:, rows] = True
+    assert_close(out, want, dtype, what, mask=mask)
+    # the call without key split takes the same tiles whole; one-token rows
+    # run on the decode kernel either way
+    ref = _unsplit(ops, q, meta, wd, monkeypatch)
+    assert_close(out, ref.float().cpu().numpy(), dtype, what + " vs unsplit")
