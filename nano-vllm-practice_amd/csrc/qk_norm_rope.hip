@@ -53,6 +53,27 @@ __device__ __forceinline__ void store8(F32, char* p, const float f[8]) {
     st16(p + 16, u32x4{__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7])});
 }
 
+// Source row of row slot pi of tokens t0..: q head, k head or v head.
+// Plain values in, so the three-way choice stays a register select (a
+// choice among the kernel argument's fields, read through the lambdas'
+// captures, compiled to a load from the argument block or from scratch at
+// every use).
+struct RowSrc {
+    uint64_t base[3];
+    int64_t tok[3], head[3];
+};
+template <int EB>
+__device__ __forceinline__ const char* row_src(const RowSrc rs, int pi, int R, int H, int KVH, int t0, int d0) {
+    const int ti = pi / R;
+    const int r = pi - ti * R;
+    const bool isq = r < H, isk = !isq && r < H + KVH;
+    const int hr = isq ? r : isk ? r - H : r - H - KVH;
+    const int64_t stt = isq ? rs.tok[0] : isk ? rs.tok[1] : rs.tok[2];
+    const int64_t sth = isq ? rs.head[0] : isk ? rs.head[1] : rs.head[2];
+    const uint64_t base = isq ? rs.base[0] : isk ? rs.base[1] : rs.base[2];
+    return reinterpret_cast<const char*>(base) + ((int64_t)(t0 + ti) * stt + (int64_t)hr * sth + d0) * EB;
+}
+
 // Raw 16-byte chunks of one row slice (two for f32: 8 floats).
 template <typename E>
 struct RowRaw {
@@ -93,10 +114,18 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
         q_begin = b;
         q_end = b + 1;
     }
-    // max_q_len only sizes the grid: a sequence longer than it is covered
-    // by later rounds of the same workgroups (the loop condition is uniform
-    // across the workgroup, so the barriers inside stay matched).
-    for (int t0 = q_begin + (int)blockIdx.x * kProTokens; t0 < q_end; t0 += (int)gridDim.x * kProTokens) {
+    const RowSrc rsrc{{(uint64_t)(uintptr_t)a.q, (uint64_t)(uintptr_t)a.cw.k, (uint64_t)(uintptr_t)a.cw.v},
+                      {a.q_stride_token, a.cw.k_stride_token, a.cw.v_stride_token},
+                      {a.q_stride_head, a.cw.k_stride_head, a.cw.v_stride_head}};
+
+    // One round: tokens t0 .. t0 + kProTokens - 1 of the sequence; the first
+    // keeps two batches of rows in flight, later ones (a sequence longer
+    // than the max_q_len that sized the grid) load one row per DPP row at a
+    // time, so that rarely used path does not raise the register count
+    // (one loop around a single copy of the code needed ~220 registers, two
+    // waves per SIMD instead of four: 34 instead of 22.6 us per 8 x 512 chunk).
+    auto round = [&](int t0, auto two_c) __attribute__((always_inline)) {
+    constexpr bool kTwo = decltype(two_c)::value;
     const int t1 = min(q_end, t0 + kProTokens);
     const int ntok = t1 - t0;
     const int tid = threadIdx.x;
@@ -108,23 +137,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int R = H + 2 * KVH;  // rows per token: q heads, k heads, v heads
     const int pairs = ntok * R;
 
-    // Source of row pi (token t0 + pi / R): q head, k head or v head.
-    auto src_of = [&](int pi) -> const char* {
-        const int ti = pi / R;
-        const int r = pi - ti * R;
-        const int t = t0 + ti;
-        if (r < H)
-            return static_cast<const char*>(a.q) + ((int64_t)t * a.q_stride_token + (int64_t)r * a.q_stride_head + d0) * EB;
-        if (r < H + KVH)
-            return static_cast<const char*>(a.cw.k) +
-                   ((int64_t)t * a.cw.k_stride_token + (int64_t)(r - H) * a.cw.k_stride_head + d0) * EB;
-        return static_cast<const char*>(a.cw.v) +
-               ((int64_t)t * a.cw.v_stride_token + (int64_t)(r - H - KVH) * a.cw.v_stride_head + d0) * EB;
-    };
+    auto src_of = [&](int pi) { return row_src<EB>(rsrc, pi, R, H, KVH, t0, d0); };
     // A batch is kProBatch rows per DPP row (128 rows per workgroup).
-    auto load_batch = [&](int base, RowRaw<E>(&raw)[kProBatch]) {
+    auto load_batch = [&](int base, auto& raw) {
+        constexpr int N = sizeof(raw) / sizeof(raw[0]);
 #pragma unroll
-        for (int k = 0; k < kProBatch; ++k) {
+        for (int k = 0; k < N; ++k) {
             const int pi = base + lrow + 16 * k;
             if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
         }
@@ -134,8 +152,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     // go out before anything else, so the position and block-table lookups
     // below wait while the rows are already on their way.
     RowRaw<E> ra[kProBatch], rb[kProBatch];
-    load_batch(0, ra);
-    if (pairs > 16 * kProBatch) load_batch(16 * kProBatch, rb);
+    if constexpr (kTwo) {
+        load_batch(0, ra);
+        if (pairs > 16 * kProBatch) load_batch(16 * kProBatch, rb);
+    }
 
     // This thread's share of the tokens' cos / sin rows: tokens tid / 64 + 4i,
     // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.
@@ -149,7 +169,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int p0 = a.cw.positions[q_begin];
     const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
     const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
-    __syncthreads();  // the previous round's readers of s_stop / s_blk / s_rope are done
+    if constexpr (!kTwo) __syncthreads();  // the previous round's readers of s_stop / s_blk / s_rope are done
     if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
     __syncthreads();
     if (p0 >= 0) {
@@ -179,9 +199,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     const int stop = s_stop;
 
     // Norm, rotate and store one batch.
-    auto process = [&](int base, const RowRaw<E>(&raw)[kProBatch]) {
+    auto process = [&](int base, const auto& raw) {
+        constexpr int N = sizeof(raw) / sizeof(raw[0]);
 #pragma unroll
-        for (int k = 0; k < kProBatch; ++k) {
+        for (int k = 0; k < N; ++k) {
             const int pi = base + lrow + 16 * k;  // uniform within the DPP row
             if (pi >= pairs) break;
             const int ti = pi / R;
@@ -234,15 +255,31 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
 
     // Two batches in flight: each buffer is refilled as soon as its batch is stored.
     constexpr int kB = 16 * kProBatch;
-    for (int base = 0; base < pairs; base += 2 * kB) {
-        process(base, ra);
-        if (base + 2 * kB < pairs) load_batch(base + 2 * kB, ra);
-        if (base + kB < pairs) {
-            process(base + kB, rb);
-            if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
+    if constexpr (kTwo) {
+        for (int base = 0; base < pairs; base += 2 * kB) {
+            process(base, ra);
+            if (base + 2 * kB < pairs) load_batch(base + 2 * kB, ra);
+            if (base + kB < pairs) {
+                process(base + kB, rb);
+                if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
+            }
+        }
+    } else {
+        RowRaw<E> r1[1];
+        for (int base = 0; base < pairs; base += 16) {
+            load_batch(base, r1);
+            process(base, r1);
         }
     }
-    }
+    };
+    // max_q_len only sizes the grid: a sequence longer than it is covered by
+    // later rounds of the same workgroups (the loop condition is uniform
+    // across the workgroup, so the barriers inside stay matched).
+    const int first = q_begin + (int)blockIdx.x * kProTokens;
+    if (first >= q_end) return;
+    round(first, std::true_type{});
+    for (int t0 = first + (int)gridDim.x * kProTokens; t0 < q_end; t0 += (int)gridDim.x * kProTokens)
+        round(t0, std::false_type{});
 }
 
 hipError_t launch_qk_norm_rope(int dtype, const PrologueArgs& a, int max_q_len, hipStream_t st) {
