@@ -125,152 +125,152 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(PrologueArgs a) {
     // (one loop around a single copy of the code needed ~220 registers, two
     // waves per SIMD instead of four: 34 instead of 22.6 us per 8 x 512 chunk).
     auto round = [&](int t0, auto two_c) __attribute__((always_inline)) {
-    constexpr bool kTwo = decltype(two_c)::value;
-    const int t1 = min(q_end, t0 + kProTokens);
-    const int ntok = t1 - t0;
-    const int tid = threadIdx.x;
+        constexpr bool kTwo = decltype(two_c)::value;
+        const int t1 = min(q_end, t0 + kProTokens);
+        const int ntok = t1 - t0;
+        const int tid = threadIdx.x;
 
-    const int lrow = tid >> 4;  // DPP row of the workgroup: one (token, head row) at a time
-    const int c = tid & 15;     // dims 8c .. 8c + 7
-    const int d0 = 8 * c;
-    const int H = a.n_heads, KVH = a.cw.n_kv_heads;
-    const int R = H + 2 * KVH;  // rows per token: q heads, k heads, v heads
-    const int pairs = ntok * R;
+        const int lrow = tid >> 4;  // DPP row of the workgroup: one (token, head row) at a time
+        const int c = tid & 15;     // dims 8c .. 8c + 7
+        const int d0 = 8 * c;
+        const int H = a.n_heads, KVH = a.cw.n_kv_heads;
+        const int R = H + 2 * KVH;  // rows per token: q heads, k heads, v heads
+        const int pairs = ntok * R;
 
-    auto src_of = [&](int pi) { return row_src<EB>(rsrc, pi, R, H, KVH, t0, d0); };
-    // A batch is kProBatch rows per DPP row (128 rows per workgroup).
-    auto load_batch = [&](int base, auto& raw) {
-        constexpr int N = sizeof(raw) / sizeof(raw[0]);
+        auto src_of = [&](int pi) { return row_src<EB>(rsrc, pi, R, H, KVH, t0, d0); };
+        // A batch is kProBatch rows per DPP row (128 rows per workgroup).
+        auto load_batch = [&](int base, auto& raw) {
+            constexpr int N = sizeof(raw) / sizeof(raw[0]);
 #pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const int pi = base + lrow + 16 * k;
-            if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
-        }
-    };
-
-    // The first two batches of rows depend only on cu_seqlens: their loads
-    // go out before anything else, so the position and block-table lookups
-    // below wait while the rows are already on their way.
-    RowRaw<E> ra[kProBatch], rb[kProBatch];
-    if constexpr (kTwo) {
-        load_batch(0, ra);
-        if (pairs > 16 * kProBatch) load_batch(16 * kProBatch, rb);
-    }
-
-    // This thread's share of the tokens' cos / sin rows: tokens tid / 64 + 4i,
-    // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.
-    const int rt = tid >> 6, rsel = (tid >> 5) & 1, rd = 4 * (tid & 31);
-    int pr[kProTokens / 4];
-#pragma unroll
-    for (int i = 0; i < kProTokens / 4; ++i) pr[i] = rt + 4 * i < ntok ? a.positions_rope[t0 + rt + 4 * i] : -1;
-
-    // Destination pages of this workgroup's tokens (as kv_cache_write_kernel;
-    // they touch at most two pages).
-    const int p0 = a.cw.positions[q_begin];
-    const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
-    const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
-    if constexpr (!kTwo) __syncthreads();  // the previous round's readers of s_stop / s_blk / s_rope are done
-    if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
-    __syncthreads();
-    if (p0 >= 0) {
-        const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
-        for (int tc = p0 / kPage + tid; tc <= colB; tc += 256) {
-            const int blk = tc < a.cw.num_pages_per_seq ? table[tc] : -1;
-            if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, tc);
-            if (tc == colA) s_blk[0] = blk;
-            if (tc == colB) s_blk[1] = blk;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kProTokens / 4; ++i) {
-        float4 v4;
-        if (pr[i] >= 0 && pr[i] < a.rope_rows) {
-            const float* tab = rsel ? a.sin : a.cos;
-            v4 = *reinterpret_cast<const float4*>(tab + (int64_t)pr[i] * a.rope_stride + rd);
-        } else {  // a position outside the tables: NaN rows
-            v4 = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
-        }
-        if (rt + 4 * i < ntok) *reinterpret_cast<float4*>(&s_rope[rt + 4 * i][rsel][rd]) = v4;
-    }
-    float wq[8], wk[8];
-    load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
-    load8(E{}, static_cast<const char*>(a.k_weight) + d0 * EB, wk);
-    __syncthreads();
-    const int stop = s_stop;
-
-    // Norm, rotate and store one batch.
-    auto process = [&](int base, const auto& raw) {
-        constexpr int N = sizeof(raw) / sizeof(raw[0]);
-#pragma unroll
-        for (int k = 0; k < N; ++k) {
-            const int pi = base + lrow + 16 * k;  // uniform within the DPP row
-            if (pi >= pairs) break;
-            const int ti = pi / R;
-            const int r = pi - ti * R;
-            const int t = t0 + ti;
-            const int pc = p0 + (t - q_begin);  // cache position
-            const int col = pc / kPage;
-            const bool write_cache = p0 >= 0 && col < stop;
-            char* dst = nullptr;
-            if (r >= H && write_cache) {
-                const int h = r < H + KVH ? r - H : r - H - KVH;
-                const int blk = s_blk[col == colA ? 0 : 1];
-                const int64_t el = (int64_t)blk * a.cw.pool_stride_block + (int64_t)h * a.cw.pool_stride_head +
-                                   (int64_t)(pc % kPage) * a.cw.pool_stride_row + d0;
-                dst = static_cast<char*>(r < H + KVH ? a.cw.k_pool : a.cw.v_pool) + el * EB;
+            for (int k = 0; k < N; ++k) {
+                const int pi = base + lrow + 16 * k;
+                if (pi < pairs) load_raw<E>(src_of(pi), raw[k]);
             }
-            if (r >= H + KVH) {  // v: plain copy
-                if (dst) store_raw<E>(dst, raw[k]);
-                continue;
-            }
-            const bool is_q = r < H;
-            float x[8];
-            raw_to_float(E{}, raw[k], x);
-            // RMSNorm over the 128 dims of the row.
-            float ss = 0.0f;
+        };
+
+        // The first two batches of rows depend only on cu_seqlens: their loads
+        // go out before anything else, so the position and block-table lookups
+        // below wait while the rows are already on their way.
+        RowRaw<E> ra[kProBatch], rb[kProBatch];
+        if constexpr (kTwo) {
+            load_batch(0, ra);
+            if (pairs > 16 * kProBatch) load_batch(16 * kProBatch, rb);
+        }
+
+        // This thread's share of the tokens' cos / sin rows: tokens tid / 64 + 4i,
+        // table (tid / 32) % 2, dims 4 (tid % 32) .. + 3.
+        const int rt = tid >> 6, rsel = (tid >> 5) & 1, rd = 4 * (tid & 31);
+        int pr[kProTokens / 4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-            ss = row16_sum(ss);
-            const float rinv = 1.0f / sqrtf(ss * (1.0f / kDimHead) + a.eps);
-            const float* w = is_q ? wq : wk;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) x[i] = x[i] * rinv * w[i];
-            // RoPE at this token's position: rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] above.
-            float o[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float partner = dpp_f32<0x128>(x[i]);  // lane c +- 8 (row_ror:8)
-                const float rot = c < 8 ? -partner : partner;
-                o[i] = fmaf(s_rope[ti][0][d0 + i], x[i], s_rope[ti][1][d0 + i] * rot);
-            }
-            if (is_q) {
-                char* qo = static_cast<char*>(a.q_out) +
-                           ((int64_t)t * a.q_out_stride_token + (int64_t)r * a.q_out_stride_head + d0) * EB;
-                store8(E{}, qo, o);
-            } else if (dst) {
-                store8(E{}, dst, o);
+        for (int i = 0; i < kProTokens / 4; ++i) pr[i] = rt + 4 * i < ntok ? a.positions_rope[t0 + rt + 4 * i] : -1;
+
+        // Destination pages of this workgroup's tokens (as kv_cache_write_kernel;
+        // they touch at most two pages).
+        const int p0 = a.cw.positions[q_begin];
+        const int colA = p0 >= 0 ? (p0 + (t0 - q_begin)) / kPage : 0;
+        const int colB = p0 >= 0 ? (p0 + (t1 - 1 - q_begin)) / kPage : 0;
+        if constexpr (!kTwo) __syncthreads();  // the previous round's readers of s_stop / s_blk / s_rope are done
+        if (tid == 0) s_stop = p0 < 0 ? -1 : 0x7fffffff;
+        __syncthreads();
+        if (p0 >= 0) {
+            const int32_t* table = a.cw.tables + (int64_t)b * a.cw.table_stride;
+            for (int tc = p0 / kPage + tid; tc <= colB; tc += 256) {
+                const int blk = tc < a.cw.num_pages_per_seq ? table[tc] : -1;
+                if (blk < 0 || (int64_t)blk >= a.cw.num_blocks) atomicMin(&s_stop, tc);
+                if (tc == colA) s_blk[0] = blk;
+                if (tc == colB) s_blk[1] = blk;
             }
         }
-    };
+#pragma unroll
+        for (int i = 0; i < kProTokens / 4; ++i) {
+            float4 v4;
+            if (pr[i] >= 0 && pr[i] < a.rope_rows) {
+                const float* tab = rsel ? a.sin : a.cos;
+                v4 = *reinterpret_cast<const float4*>(tab + (int64_t)pr[i] * a.rope_stride + rd);
+            } else {  // a position outside the tables: NaN rows
+                v4 = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+            }
+            if (rt + 4 * i < ntok) *reinterpret_cast<float4*>(&s_rope[rt + 4 * i][rsel][rd]) = v4;
+        }
+        float wq[8], wk[8];
+        load8(E{}, static_cast<const char*>(a.q_weight) + d0 * EB, wq);
+        load8(E{}, static_cast<const char*>(a.k_weight) + d0 * EB, wk);
+        __syncthreads();
+        const int stop = s_stop;
 
-    // Two batches in flight: each buffer is refilled as soon as its batch is stored.
-    constexpr int kB = 16 * kProBatch;
-    if constexpr (kTwo) {
-        for (int base = 0; base < pairs; base += 2 * kB) {
-            process(base, ra);
-            if (base + 2 * kB < pairs) load_batch(base + 2 * kB, ra);
-            if (base + kB < pairs) {
-                process(base + kB, rb);
-                if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
+        // Norm, rotate and store one batch.
+        auto process = [&](int base, const auto& raw) {
+            constexpr int N = sizeof(raw) / sizeof(raw[0]);
+#pragma unroll
+            for (int k = 0; k < N; ++k) {
+                const int pi = base + lrow + 16 * k;  // uniform within the DPP row
+                if (pi >= pairs) break;
+                const int ti = pi / R;
+                const int r = pi - ti * R;
+                const int t = t0 + ti;
+                const int pc = p0 + (t - q_begin);  // cache position
+                const int col = pc / kPage;
+                const bool write_cache = p0 >= 0 && col < stop;
+                char* dst = nullptr;
+                if (r >= H && write_cache) {
+                    const int h = r < H + KVH ? r - H : r - H - KVH;
+                    const int blk = s_blk[col == colA ? 0 : 1];
+                    const int64_t el = (int64_t)blk * a.cw.pool_stride_block + (int64_t)h * a.cw.pool_stride_head +
+                                       (int64_t)(pc % kPage) * a.cw.pool_stride_row + d0;
+                    dst = static_cast<char*>(r < H + KVH ? a.cw.k_pool : a.cw.v_pool) + el * EB;
+                }
+                if (r >= H + KVH) {  // v: plain copy
+                    if (dst) store_raw<E>(dst, raw[k]);
+                    continue;
+                }
+                const bool is_q = r < H;
+                float x[8];
+                raw_to_float(E{}, raw[k], x);
+                // RMSNorm over the 128 dims of the row.
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+                ss = row16_sum(ss);
+                const float rinv = 1.0f / sqrtf(ss * (1.0f / kDimHead) + a.eps);
+                const float* w = is_q ? wq : wk;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) x[i] = x[i] * rinv * w[i];
+                // RoPE at this token's position: rot(x)[d] = -x[d + 64] for d < 64, x[d - 64] above.
+                float o[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float partner = dpp_f32<0x128>(x[i]);  // lane c +- 8 (row_ror:8)
+                    const float rot = c < 8 ? -partner : partner;
+                    o[i] = fmaf(s_rope[ti][0][d0 + i], x[i], s_rope[ti][1][d0 + i] * rot);
+                }
+                if (is_q) {
+                    char* qo = static_cast<char*>(a.q_out) +
+                               ((int64_t)t * a.q_out_stride_token + (int64_t)r * a.q_out_stride_head + d0) * EB;
+                    store8(E{}, qo, o);
+                } else if (dst) {
+                    store8(E{}, dst, o);
+                }
+            }
+        };
+
+        // Two batches in flight: each buffer is refilled as soon as its batch is stored.
+        constexpr int kB = 16 * kProBatch;
+        if constexpr (kTwo) {
+            for (int base = 0; base < pairs; base += 2 * kB) {
+                process(base, ra);
+                if (base + 2 * kB < pairs) load_batch(base + 2 * kB, ra);
+                if (base + kB < pairs) {
+                    process(base + kB, rb);
+                    if (base + 3 * kB < pairs) load_batch(base + 3 * kB, rb);
+                }
+            }
+        } else {
+            RowRaw<E> r1[1];
+            for (int base = 0; base < pairs; base += 16) {
+                load_batch(base, r1);
+                process(base, r1);
             }
         }
-    } else {
-        RowRaw<E> r1[1];
-        for (int base = 0; base < pairs; base += 16) {
-            load_batch(base, r1);
-            process(base, r1);
-        }
-    }
     };
     // max_q_len only sizes the grid: a sequence longer than it is covered by
     // later rounds of the same workgroups (the loop condition is uniform
