@@ -51,6 +51,29 @@ def test_dense_attention(C, gpu, dtype, shape):
     assert_close(out, want, dtype, f"dense {shape} {dtype}")
 
 
+DENSE_HEADS = [(2, 2), (4, 4), (8, 2), (16, 8), (32, 8), (12, 4), (6, 2), (5, 1), (3, 3), (64, 8)]
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_dense_attention_random_shapes(C, gpu, seed):
+    """Seeded random shapes: batch 1-4, ten head layouts, query and key
+    lengths from 1 to a few hundred (ragged against the 32-, 64- or
+    128-row query tiles and the 64-key tiles), f16 and bf16."""
+    rng = np.random.default_rng(500 + seed)
+    H, KVH = DENSE_HEADS[int(rng.integers(len(DENSE_HEADS)))]
+    B = int(rng.integers(1, 5))
+    Tq = int(rng.choice([1, int(rng.integers(2, 64)), int(rng.integers(64, 300))]))
+    Tkv = int(rng.choice([1, int(rng.integers(2, 128)), int(rng.integers(128, 700))]))
+    dtype = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+    q = rand((B, H, Tq, 128), dtype, 600 + seed)
+    k = rand((B, KVH, Tkv, 128), dtype, 700 + seed)
+    v = rand((B, KVH, Tkv, 128), dtype, 800 + seed)
+    out = C.FlashAttentionWarpCuda(q.to(gpu), k.to(gpu), v.to(gpu))
+    torch.cuda.synchronize()
+    want = oa.dense_attention(np64(q), np64(k), np64(v))
+    assert_close(out, want, dtype, f"dense B={B} H={H} KVH={KVH} Tq={Tq} Tkv={Tkv} {dtype}")
+
+
 def test_dense_equals_paged_identity_table(C, ops, gpu):
     """Dense attention == paged prefill with contiguous pages and no causal limit."""
     B, H, KVH, T = 1, 8, 4, 96
