@@ -86,3 +86,53 @@ def test_random_batch(ops, gpu, monkeypatch, seed):
     # run on the decode kernel either way
     ref = _unsplit(ops, q, meta, wd, monkeypatch)
     assert_close(out, ref.float().cpu().numpy(), dtype, what + " vs unsplit")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+def test_random_batch_arbitrary_positions(ops, gpu, monkeypatch, seed):
+    """The same kind of batches with each token's position drawn anywhere:
+    mostly inside its context, a few past it (all keys visible) and a few at
+    -1 (no key visible: a NaN row, as in the reference).  Key pieces then
+    see fewer or more key tiles than the engine's layout implies, and
+    some rows of a piece see none."""
+    chunks, H, KVH, dtype = random_batch(7500 + seed)
+    what = f"seed {7500 + seed}: H={H} KVH={KVH} {dtype} chunks {chunks}, arbitrary positions"
+    print(what, flush=True)
+    w = workloads.make_paged_workload("random_pos", chunks, H, KVH, dtype=dtype, seed=7500 + seed)
+    q, meta = w.gemm_call(device=gpu)
+    rng = np.random.default_rng(7500 + seed)
+    cu = meta.raw_cu_seqlens
+    pos = np.asarray(meta.raw_positions).copy()
+    for b, kvl in enumerate(meta.kv_lens.tolist()):
+        for t in range(cu[b], cu[b + 1]):
+            r = rng.random()
+            pos[t] = -1 if r < 0.05 else kvl + int(rng.integers(0, 50)) if r < 0.1 else int(rng.integers(0, max(1, kvl)))
+    meta.raw_positions = [int(x) for x in pos]
+    meta.positions = torch.tensor(pos, dtype=torch.int32, device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    out = _gemm(ops, q, meta, wd)
+    assert _workspace_is_zero(gpu), f"split counters not reset after {what}"
+    work = sum((cu[b + 1] - cu[b]) * (p + n) for b, (p, n) in enumerate(chunks)) * H
+    rows = None
+    if work > FULL_CHECK:
+        rows = sorted(set(sample_rows(cu, 12, np.random.default_rng(seed))))
+    want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), cu, np_tables(meta),
+                            meta.kv_lens.tolist(), pos, rows=rows)
+    mask = None
+    if rows is not None:
+        mask = np.zeros(want.shape, dtype=bool)
+        mask[:, rows] = True
+    assert_close(out, want, dtype, what, mask=mask)
+    # Without key split: the oracle's bar too, and at most one output unit
+    # in the last place from the split result (rows that see a few keys
+    # reach magnitudes of 2-4, where a bf16 unit is 2^-6, and the split's
+    # partials can move a value across a rounding boundary).
+    ref = _unsplit(ops, q, meta, wd, monkeypatch)
+    assert_close(ref, want, dtype, what + ", unsplit", mask=mask)
+    a, b = np64(out), np64(ref)
+    ulp = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -10}[dtype]  # relative spacing bound
+    both = ~(np.isnan(a) | np.isnan(b))
+    assert np.array_equal(np.isnan(a), np.isnan(b)), what + ": NaN rows differ from the unsplit call"
+    assert np.all(np.abs(a - b)[both] <= 1e-2 + ulp * np.maximum(np.abs(a), np.abs(b))[both]), what + " vs unsplit"
