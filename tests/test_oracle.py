@@ -467,3 +467,46 @@ def test_rope_tables_match_float64_angles():
     for cos, sin in (tuple(t.numpy() for t in rope_tables(P, D)), op.rope_tables(P, D)):
         assert np.all(np.abs(cos - np.cos(theta)) <= bound)
         assert np.all(np.abs(sin - np.sin(theta)) <= bound)
+
+
+def test_sdpa_path_decode_matches_oracle():
+    """The torch restatement of the reference CPU decode path agrees with the oracle."""
+    rng = np.random.default_rng(12)
+    kv_lens = [17, 64, 200, 1]
+    k_pool, v_pool, tables, _, _ = build_paged(rng, kv_lens, 4, 32, 24)
+    q = rng.standard_normal((8, len(kv_lens), 32))
+    want = oa.paged_decode(q, k_pool, v_pool, tables, kv_lens)
+    got = sdpa_path.paged_decode(torch.from_numpy(q), torch.from_numpy(k_pool), torch.from_numpy(v_pool),
+                                 tables.tolist(), kv_lens)
+    np.testing.assert_allclose(got.numpy(), want, atol=1e-12)
+
+
+def test_sdpa_path_dense_matches_oracle():
+    """The torch restatement of the dense entry (GQA, non-causal) agrees with the oracle."""
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((2, 8, 9, 16))
+    k = rng.standard_normal((2, 2, 13, 16))
+    v = rng.standard_normal((2, 2, 13, 16))
+    got = sdpa_path.dense_attention(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v))
+    np.testing.assert_allclose(got.numpy(), oa.dense_attention(q, k, v), atol=1e-12)
+
+
+def test_row_bound_has_power_at_131072_keys():
+    """At 131,072 keys the outputs are small (RMS ~ 1/sqrt(keys)), so max-abs 1e-2
+    alone accepts an answer scaled by 0.9 (or 0.5); the per-row scale-aware bound
+    of the parity helper rejects it, and accepts the bf16 rounding of the answer."""
+    from femtovllm import workloads
+    from helpers import assert_close, np32, np64, np_tables
+
+    L = 131072
+    w = workloads.make_paged_workload("row_bound", [(L - 1, 1)], 4, 1, seed=31)
+    q, meta = w.gemv_call()
+    want = oa.paged_decode(np64(q), np32(w.k_pool), np32(w.v_pool), np_tables(meta), meta.kv_lens.tolist())
+    assert np.abs(want).max() < 0.05  # the regime where max-abs 1e-2 is weak
+    rounded = torch.from_numpy(want).to(torch.bfloat16)
+    assert_close(rounded, want, torch.bfloat16, "bf16 rounding of the oracle")
+    for factor in (0.9, 0.5):
+        scaled = torch.from_numpy(want * factor).to(torch.bfloat16)
+        assert np.abs(np64(scaled) - want).max() <= 1e-2  # max-abs alone would pass
+        with pytest.raises(AssertionError, match="per-row bound"):
+            assert_close(scaled, want, torch.bfloat16, f"oracle x {factor}")

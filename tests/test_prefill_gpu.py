@@ -93,6 +93,25 @@ def test_long_context_chunks(ops, gpu, long_context, chunk):
     assert_close(out, want, torch.bfloat16, f"long-context chunk {chunk}", mask=mask)
 
 
+@pytest.mark.parametrize("chunk", [0, 7, 15])
+def test_long_context_chunks_every_row(ops, gpu, long_context, chunk):
+    """Every row of the first, a middle and the last 2048-token chunk (32 heads,
+    up to 32,768 keys), under the scale-aware per-row bound; the oracle runs over
+    512-row slices to bound its memory."""
+    w, wd, kp, vp = long_context
+    q, meta = workloads.long_context_chunk(w, chunk, device=gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    qn, tables = np64(q), np_tables(meta)
+    want = np.empty(tuple(out.shape), dtype=np.float64)
+    for r0 in range(0, out.shape[1], 512):
+        rows = list(range(r0, min(out.shape[1], r0 + 512)))
+        part = oa.paged_prefill(qn, kp, vp, meta.raw_cu_seqlens, tables, meta.kv_lens.tolist(),
+                                np.asarray(meta.raw_positions), rows=rows)
+        want[:, rows] = part[:, rows]
+    err = assert_close(out, want, torch.bfloat16, f"long-context chunk {chunk}, every row")
+    print(f"chunk {chunk}: max abs err {err:.2e}")
+
+
 @pytest.fixture(scope="module")
 def mixed(gpu):
     """The unified Qwen3-8B-shaped batch and the oracle for every row of it.
