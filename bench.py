@@ -248,6 +248,11 @@ def main():
         assert not torch.isnan(out.float()).any(), "decode produced NaN"
         mean_ms, med_ms, wall = timer.run(fn, K, W)
         wf_ms, _, _ = timer.run(fn, K, 1, write_flush=True)
+        prev = _C._lib.femto_attn_set_decode_single_max_kv(1 << 30)
+        try:
+            one_launch_ms, _, _ = timer.run(fn, K, W)
+        finally:
+            _C._lib.femto_attn_set_decode_single_max_kv(prev)
         nbytes = workloads.decode_bytes(w)
         gbs = nbytes / (mean_ms * 1e-3) / 1e9
         traffic, traffic_source = pmc_traffic("paged_decode_bf16_qwen3_0.6b_b64", DECODE_SOURCES)
@@ -288,6 +293,7 @@ def main():
             },
             "median_ms_per_step": round(med_ms, 5),
             "ms_per_step_write_flush": round(wf_ms, 5),
+            "ms_per_step_one_launch_route": round(one_launch_ms, 5),
             "wall_s_timed_region": round(wall, 3),
         }
         del wd
@@ -296,23 +302,38 @@ def main():
         del w
 
         # The reference's CPU-runnable case: fp32, 4 sequences, contexts
-        # {17, 64, 200, 511}; launch-bound (a few MB), so reported as latency.
-        w = workloads.decode_fp32_small(poison=False)
-        wd = w.to(dev)
-        q, meta = wd.gemv_call(device=dev)
-        fn = lambda: ops.paged_attention_gemv(q, wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
-                                              meta.max_kv_len)
-        mean_ms, med_ms, _ = timer.run(fn, K, W)
-        nbytes = workloads.decode_bytes(w)
-        gbs = nbytes / (mean_ms * 1e-3) / 1e9
-        extra.append({
-            "workload": "paged_decode_fp32_4seqs_ctx17-511_h16_kv8", "metric": "ms per call",
-            "value": round(mean_ms, 5), "median_ms": round(med_ms, 5),
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nbytes,
-                         "note": "launch-bound: two kernel launches for a few MB"},
-        })
-        del wd, w
+        # {17, 64, 200, 511}, and a 64-sequence step of short contexts; both
+        # launch-bound (a few MB), so reported as latency.  Each is timed on
+        # both decode routes (one launch; split workers + merge) as well as
+        # with the library's default choice, which picks the route by
+        # max_kv_len.
+        def route_ms(fn, limit):
+            prev = _C._lib.femto_attn_set_decode_single_max_kv(limit)
+            try:
+                return timer.run(fn, K, W)[0]
+            finally:
+                _C._lib.femto_attn_set_decode_single_max_kv(prev)
+
+        for name, make in (("paged_decode_fp32_4seqs_ctx17-511_h16_kv8", workloads.decode_fp32_small),
+                           ("paged_decode_bf16_64seqs_ctx64-512_h16_kv8", workloads.decode_bf16_short)):
+            w = make(poison=False)
+            wd = w.to(dev)
+            q, meta = wd.gemv_call(device=dev)
+            fn = lambda: ops.paged_attention_gemv(q, wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
+                                                  meta.max_kv_len)
+            mean_ms, med_ms, _ = timer.run(fn, K, W)
+            nbytes = workloads.decode_bytes(w)
+            gbs = nbytes / (mean_ms * 1e-3) / 1e9
+            extra.append({
+                "workload": name, "metric": "ms per call",
+                "value": round(mean_ms, 5), "median_ms": round(med_ms, 5),
+                "max_kv_len": int(meta.max_kv_len),
+                "ms_one_launch": round(route_ms(fn, 1 << 30), 5), "ms_split_plus_merge": round(route_ms(fn, -1), 5),
+                "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": nbytes,
+                             "note": "latency-bound: a few MB per call"},
+            })
+            del wd, w
 
     # ---------------- prefill: 8 x 512 chunks -----------------------------
     if want("prefill"):

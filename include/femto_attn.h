@@ -49,19 +49,30 @@ int femto_attn_max_kv_len_non_split(void);
 int femto_attn_kv_len_per_page(void);
 int femto_attn_dim_head(void);
 
-/* Bytes of workspace femto_paged_attention_gemv needs for these sizes
- * (0 when no sequence is split).  It holds the per-split partial softmax
- * states between the split kernel and the merge kernel of one call; no
- * initialisation is needed.  Calls that may overlap (other streams) must
- * not share a workspace. */
+/* Bytes of workspace femto_paged_attention_gemv needs for these sizes when
+ * it runs split (max_kv_len above the one-launch limit below).  It holds the
+ * per-split partial softmax states between the split kernel and the merge
+ * kernel of one call; no initialisation is needed.  Calls that may overlap
+ * (other streams) must not share a workspace. */
 size_t femto_paged_attention_gemv_workspace_size(int num_seqs, int n_heads, int max_kv_len);
+
+/* Decode calls with max_kv_len at most this limit (default 1024 keys) run as
+ * one kernel launch (a workgroup per sequence and KV head group) and use no
+ * workspace; longer ones run the split kernel and the merge kernel.  Sets the
+ * limit for the process (-1: always split) and returns the previous one.
+ * No counterpart in the reference (whose decode is always one launch,
+ * csrc/paged_attention/paged_attention_gemv.cu:280-300); it exists for tests
+ * and tuning. */
+int femto_attn_set_decode_single_max_kv(int max_kv_len);
 
 /* Paged decode attention: one query token per sequence attends to all
  * kv_lens[b] keys of its block table; GQA kv head = h / (n_heads / n_kv_heads).
  * Replaces PagedAttentionGemvCuda (csrc/paged_attention/paged_attention_gemv.cu:223-308),
  * bound as _C.PagedAttentionGemvCuda (csrc/bindings.cpp:52-59, 94-97) and
  * called by femtovllm.ops.paged_attention_gemv (femtovllm/ops/__init__.py:82-107).
- * dtype: F32, F16 or BF16.  kv_len == 0 yields a zero row, as in the reference. */
+ * dtype: F32, F16 or BF16.  kv_len == 0 yields a zero row, as in the reference.
+ * workspace may be NULL (0 bytes) when max_kv_len is within the one-launch
+ * limit of femto_attn_set_decode_single_max_kv. */
 int femto_paged_attention_gemv(
     int dtype,
     const void* q, int64_t q_stride_head, int64_t q_stride_seq,

@@ -215,6 +215,177 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int b) {
     return len;
 }
 
+// Softmax state of query heads h0 .. h0+NREP-1 of sequence b over pages
+// [lp0, lp0 + n) of its kv_len keys (query row qrow): the running max m
+// (log2 units), the row sum l and the 8 unnormalised accumulators of this
+// lane's dims.  On return every lane holds the state of the whole wave for
+// its dims (lane & 15).  Used by the split workers (one segment of a slice)
+// and by the one-launch kernel (a quarter of a sequence per wave).
+template <typename E, int NREP>
+__device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int kv_len, int lp0, int n, int qrow,
+                                               int h0, int64_t head_off, float (&m)[NREP], float (&l)[NREP],
+                                               float (&acc)[NREP][8]) {
+    constexpr int EB = E::kBytes;
+    const int lane = threadIdx.x & 63;
+    const int rg = lane >> 4;
+    const int c = lane & 15;
+    const char* qbase = reinterpret_cast<const char*>(a.q);
+    const char* kpool = reinterpret_cast<const char*>(a.k_pool);
+    const char* vpool = reinterpret_cast<const char*>(a.v_pool);
+    RowSlice<E> qs[NREP];
+#pragma unroll
+    for (int r = 0; r < NREP; ++r)
+        qs[r].load(qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)qrow * a.q_stride_seq) * EB, c);
+#pragma unroll
+    for (int r = 0; r < NREP; ++r) {
+        m[r] = kEmptyMax;
+        l[r] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+    }
+
+    const int32_t* table = a.tables + (int64_t)b * a.table_stride;
+    int tbl = -1;
+    auto fetch_table = [&](int i0) {
+        const int pg = lp0 + i0 + lane;
+        tbl = (i0 + lane < n && pg < a.num_pages_per_seq) ? table[pg] : -1;
+    };
+    // The 8 (f32: 16) 16-byte loads of page lp0 + i.  Rows past kv_len
+    // are clamped to the last visible row and blocks outside the pool to
+    // block 0, so every load is in bounds and unconditional; those values
+    // are never used (masked scores, zeroed registers).
+    auto issue = [&](int i, PageRegs<E>& pr, bool& blk_ok) {
+        const int blk = __builtin_amdgcn_readlane(tbl, i & 63);
+        blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+        const int pg = lp0 + i;
+        const int last_row = kv_len - 1 - pg * kPage;
+        const int64_t page_off = ((int64_t)(blk_ok ? blk : 0) * a.pool_stride_block + head_off) * EB;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = min(rg + 4 * j, last_row);
+            const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
+            pr.k[j].stream(kpool + off, c);
+            pr.v[j].stream(vpool + off, c);
+        }
+    };
+    auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
+        if (!blk_ok) {
+            // A block id outside the pool reads as a page of zeros.
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pr.k[j].zero();
+                pr.v[j].zero();
+            }
+        }
+        const int pg = lp0 + i;
+        float sc[NREP][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) sc[r][j] = pr.k[j].dot(qs[r]);
+        }
+        // Raw scores (unscaled; the scale folds into the exponentials).
+        // Rows past kv_len only occur on a sequence's last page.
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) sc[r][j] = row16_sum(sc[r][j]);
+        }
+        if (pg * kPage + kPage > kv_len) {  // wave-uniform
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool valid = (pg * kPage + rg + 4 * j) < kv_len;
+#pragma unroll
+                for (int r = 0; r < NREP; ++r) sc[r][j] = valid ? sc[r][j] : -INFINITY;
+            }
+        }
+        // Lazy rescale: the running max m (log2 units) only moves when a
+        // page's max exceeds it by more than kLazyMax, so exponentials
+        // stay <= 2^kLazyMax and the accumulators are rarely rescaled.
+        const float scale = a.scale_log2;
+        auto page_max = [&](int r) {
+            return fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3])) * scale;
+        };
+        bool grow = false;
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) grow |= page_max(r) > m[r] + kLazyMax;
+        if (__ballot(grow)) {
+#pragma unroll
+            for (int r = 0; r < NREP; ++r) {
+                const float mn = fmaxf(m[r], page_max(r));
+                const float al = fast_exp2(m[r] - mn);
+                l[r] *= al;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[r][e] *= al;
+                m[r] = mn;
+            }
+        }
+        PagePV<E> pv;
+        pv.prep(pr.v);
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            float p[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p[j] = fast_exp2(fmaf(sc[r][j], scale, -m[r]));
+            pv.accumulate(p, acc[r], l[r]);
+        }
+    };
+
+    // Three pages in flight: pages i+1 and i+2 load while page i
+    // computes (96 KB of loads per CU at one wave per SIMD).
+    PageRegs<E> r0, r1, r2;
+    bool k0 = false, k1 = false, k2 = false;
+    fetch_table(0);
+    issue(0, r0, k0);
+    if (1 < n) issue(1, r1, k1);
+    for (int i = 0; i < n; i += 3) {
+        if (i + 2 < n) {
+            if (((i + 2) & 63) == 0) fetch_table(i + 2);
+            issue(i + 2, r2, k2);
+        }
+        consume(i, r0, k0);
+        if (i + 1 < n) {
+            if (i + 3 < n) {
+                if (((i + 3) & 63) == 0) fetch_table(i + 3);
+                issue(i + 3, r0, k0);
+            }
+            consume(i + 1, r1, k1);
+            if (i + 2 < n) {
+                if (i + 4 < n) {
+                    if (((i + 4) & 63) == 0) fetch_table(i + 4);
+                    issue(i + 4, r1, k1);
+                }
+                consume(i + 2, r2, k2);
+            }
+        }
+    }
+
+    // Merge the four DPP rows (same dims, different keys): rows 0+1 and
+    // 2+3, then the two halves; every lane of a pair ends with the pair's
+    // state (the first row's terms first, as row 0 computes them).
+    auto merge_pair = [&](auto pair) {
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            float m0, m1, l0, l1;
+            pair(m[r], m0, m1);
+            pair(l[r], l0, l1);
+            const float mn = fmaxf(m0, m1);
+            const float f0 = fast_exp2(m0 - mn);
+            const float f1 = fast_exp2(m1 - mn);
+            l[r] = l0 * f0 + l1 * f1;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float a0, a1;
+                pair(acc[r][e], a0, a1);
+                acc[r][e] = a0 * f0 + a1 * f1;
+            }
+            m[r] = mn;
+        }
+    };
+    merge_pair([](float x, float& a, float& b) { pair16(x, a, b); });
+    merge_pair([](float x, float& a, float& b) { pair32(x, a, b); });
+}
+
 // Load-balanced split-KV decode.  Every wave is an independent worker: the
 // pages of all sequences are concatenated (per KV head group) and cut into
 // equal slices of C pages, one slice per wave, with as many waves as the GPU
@@ -226,7 +397,6 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int b) {
 // launch, whose first workgroups are decode workers.
 template <typename E, int NREP>
 __device__ __forceinline__ void decode_waves(const DecodeArgs& a, int block) {
-    constexpr int EB = E::kBytes;
     const int lane = threadIdx.x & 63;
     const int gw = block * 4 + (threadIdx.x >> 6);
     const int grp = gw / a.waves_per_group;
@@ -274,11 +444,6 @@ __device__ __forceinline__ void decode_waves(const DecodeArgs& a, int block) {
     const uint64_t after = __ballot(base + lane < B && my_excl + pages_of(my_len) > x0);
     int b = base + __builtin_ctzll(after);
 
-    // Query rows of the NREP heads, in this lane's 8 dims (storage type).
-    RowSlice<E> qs[NREP];
-    const char* qbase = reinterpret_cast<const char*>(a.q);
-    const char* kpool = reinterpret_cast<const char*>(a.k_pool);
-    const char* vpool = reinterpret_cast<const char*>(a.v_pool);
     const int64_t head_off = (int64_t)kvh * a.pool_stride_head;
     const int H = a.n_heads;
 
@@ -306,158 +471,8 @@ __device__ __forceinline__ void decode_waves(const DecodeArgs& a, int block) {
         const int n = lp1 - lp0;
 
         const int qrow = a.cu_seqlens ? a.cu_seqlens[b] : b;
-#pragma unroll
-        for (int r = 0; r < NREP; ++r)
-            qs[r].load(qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)qrow * a.q_stride_seq) * EB, c);
         float m[NREP], l[NREP], acc[NREP][8];
-#pragma unroll
-        for (int r = 0; r < NREP; ++r) {
-            m[r] = kEmptyMax;
-            l[r] = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
-        }
-
-        const int32_t* table = a.tables + (int64_t)b * a.table_stride;
-        int tbl = -1;
-        auto fetch_table = [&](int i0) {
-            const int pg = lp0 + i0 + lane;
-            tbl = (i0 + lane < n && pg < a.num_pages_per_seq) ? table[pg] : -1;
-        };
-        // The 8 (f32: 16) 16-byte loads of page lp0 + i.  Rows past kv_len
-        // are clamped to the last visible row and blocks outside the pool to
-        // block 0, so every load is in bounds and unconditional; those values
-        // are never used (masked scores, zeroed registers).
-        auto issue = [&](int i, PageRegs<E>& pr, bool& blk_ok) {
-            const int blk = __builtin_amdgcn_readlane(tbl, i & 63);
-            blk_ok = blk >= 0 && (int64_t)blk < a.num_blocks;
-            const int pg = lp0 + i;
-            const int last_row = kv_len - 1 - pg * kPage;
-            const int64_t page_off = ((int64_t)(blk_ok ? blk : 0) * a.pool_stride_block + head_off) * EB;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = min(rg + 4 * j, last_row);
-                const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
-                pr.k[j].stream(kpool + off, c);
-                pr.v[j].stream(vpool + off, c);
-            }
-        };
-        auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
-            if (!blk_ok) {
-                // A block id outside the pool reads as a page of zeros.
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    pr.k[j].zero();
-                    pr.v[j].zero();
-                }
-            }
-            const int pg = lp0 + i;
-            float sc[NREP][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int r = 0; r < NREP; ++r) sc[r][j] = pr.k[j].dot(qs[r]);
-            }
-            // Raw scores (unscaled; the scale folds into the exponentials).
-            // Rows past kv_len only occur on a sequence's last page.
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int r = 0; r < NREP; ++r) sc[r][j] = row16_sum(sc[r][j]);
-            }
-            if (pg * kPage + kPage > kv_len) {  // wave-uniform
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool valid = (pg * kPage + rg + 4 * j) < kv_len;
-#pragma unroll
-                    for (int r = 0; r < NREP; ++r) sc[r][j] = valid ? sc[r][j] : -INFINITY;
-                }
-            }
-            // Lazy rescale: the running max m (log2 units) only moves when a
-            // page's max exceeds it by more than kLazyMax, so exponentials
-            // stay <= 2^kLazyMax and the accumulators are rarely rescaled.
-            const float scale = a.scale_log2;
-            auto page_max = [&](int r) {
-                return fmaxf(fmaxf(sc[r][0], sc[r][1]), fmaxf(sc[r][2], sc[r][3])) * scale;
-            };
-            bool grow = false;
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) grow |= page_max(r) > m[r] + kLazyMax;
-            if (__ballot(grow)) {
-#pragma unroll
-                for (int r = 0; r < NREP; ++r) {
-                    const float mn = fmaxf(m[r], page_max(r));
-                    const float al = fast_exp2(m[r] - mn);
-                    l[r] *= al;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[r][e] *= al;
-                    m[r] = mn;
-                }
-            }
-            PagePV<E> pv;
-            pv.prep(pr.v);
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) {
-                float p[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) p[j] = fast_exp2(fmaf(sc[r][j], scale, -m[r]));
-                pv.accumulate(p, acc[r], l[r]);
-            }
-        };
-
-        // Three pages in flight: pages i+1 and i+2 load while page i
-        // computes (96 KB of loads per CU at one wave per SIMD).
-        PageRegs<E> r0, r1, r2;
-        bool k0 = false, k1 = false, k2 = false;
-        fetch_table(0);
-        issue(0, r0, k0);
-        if (1 < n) issue(1, r1, k1);
-        for (int i = 0; i < n; i += 3) {
-            if (i + 2 < n) {
-                if (((i + 2) & 63) == 0) fetch_table(i + 2);
-                issue(i + 2, r2, k2);
-            }
-            consume(i, r0, k0);
-            if (i + 1 < n) {
-                if (i + 3 < n) {
-                    if (((i + 3) & 63) == 0) fetch_table(i + 3);
-                    issue(i + 3, r0, k0);
-                }
-                consume(i + 1, r1, k1);
-                if (i + 2 < n) {
-                    if (i + 4 < n) {
-                        if (((i + 4) & 63) == 0) fetch_table(i + 4);
-                        issue(i + 4, r1, k1);
-                    }
-                    consume(i + 2, r2, k2);
-                }
-            }
-        }
-
-        // Merge the four DPP rows (same dims, different keys): rows 0+1 and
-        // 2+3, then the two halves; every lane of a pair ends with the pair's
-        // state (the first row's terms first, as row 0 computes them).
-        auto merge_pair = [&](auto pair) {
-#pragma unroll
-            for (int r = 0; r < NREP; ++r) {
-                float m0, m1, l0, l1;
-                pair(m[r], m0, m1);
-                pair(l[r], l0, l1);
-                const float mn = fmaxf(m0, m1);
-                const float f0 = fast_exp2(m0 - mn);
-                const float f1 = fast_exp2(m1 - mn);
-                l[r] = l0 * f0 + l1 * f1;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    float a0, a1;
-                    pair(acc[r][e], a0, a1);
-                    acc[r][e] = a0 * f0 + a1 * f1;
-                }
-                m[r] = mn;
-            }
-        };
-        merge_pair([](float x, float& a, float& b) { pair16(x, a, b); });
-        merge_pair([](float x, float& a, float& b) { pair32(x, a, b); });
+        decode_segment<E, NREP>(a, b, kv_len, lp0, n, qrow, h0, head_off, m, l, acc);
 
         // Partial state of this segment.
         const int slot = wi - S / C;

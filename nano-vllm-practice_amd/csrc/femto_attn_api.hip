@@ -8,6 +8,7 @@
 // index dtype) live in the Python layer that owns the tensors.
 #include <algorithm>
 #include <cmath>
+#include <atomic>
 #include <mutex>
 #include <string>
 
@@ -22,6 +23,11 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 namespace {
 
 thread_local std::string g_err;
+
+// Decode calls whose max_kv_len is at most this run as one launch (a
+// workgroup per sequence and KV head group, no workspace); longer ones use
+// the split workers and the merge kernel.
+std::atomic<int> g_single_max_kv{1024};
 
 int fail(int code, const std::string& msg) {
     g_err = msg;
@@ -216,6 +222,18 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
     if (rc != FEMTO_OK) return rc;
 
     femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len, dtype);
+    if (max_kv_len <= g_single_max_kv.load(std::memory_order_relaxed)) {
+        // One launch, no workspace.  A max_kv_len below the true longest
+        // context only makes the call slower (each wave walks a quarter of
+        // its sequence, whatever the length).
+        const femto::DecodeArgs a = femto::decode_args(
+            plan, q, q_stride_head, q_stride_seq, out, out_stride_head, out_stride_seq, k_pool, v_pool, num_blocks,
+            n_kv_heads, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables,
+            num_pages_per_seq, table_stride, kv_lens, num_seqs, n_heads, nullptr);
+        return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, true,
+                                                     static_cast<hipStream_t>(stream)),
+                          (fn + " launch").c_str());
+    }
     if (use_scratch) {
         // The partial slots must fit the scratch array: with fewer slots per
         // (sequence, head) a sequence is cut into fewer, longer slices (the
@@ -247,7 +265,8 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
         plan, q, q_stride_head, q_stride_seq, out, out_stride_head, out_stride_seq, k_pool, v_pool, num_blocks,
         n_kv_heads, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables, num_pages_per_seq,
         table_stride, kv_lens, num_seqs, n_heads, workspace);
-    return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, static_cast<hipStream_t>(stream)),
+    return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, false,
+                                                 static_cast<hipStream_t>(stream)),
                       (fn + " launch").c_str());
 }
 
@@ -272,6 +291,10 @@ const char* femto_attn_last_error(void) { return g_err.c_str(); }
 int femto_attn_max_kv_len_non_split(void) { return femto::kMaxKVLenNonSplit; }
 int femto_attn_kv_len_per_page(void) { return femto::kPage; }
 int femto_attn_dim_head(void) { return femto::kDimHead; }
+
+int femto_attn_set_decode_single_max_kv(int max_kv_len) {
+    return g_single_max_kv.exchange(max_kv_len < -1 ? -1 : max_kv_len, std::memory_order_relaxed);
+}
 
 size_t femto_paged_attention_gemm_workspace_size(int num_seqs, int num_tokens, int max_q_len, int n_heads,
                                                  int n_kv_heads, int num_pages_per_seq) {
@@ -414,7 +437,7 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
                 if (a.decode_blocks <= 0) return fail(FEMTO_ERR_HIP, "paged_attention_gemm: device query");
                 a.dec = d;
             } else {
-                rc = hip_status(femto::launch_paged_decode(dtype, d, plan.nrep_tile, num_seqs, st),
+                rc = hip_status(femto::launch_paged_decode(dtype, d, plan.nrep_tile, num_seqs, false, st),
                                 "paged_attention_gemm decode-row launch");
                 if (rc != FEMTO_OK) return rc;
             }

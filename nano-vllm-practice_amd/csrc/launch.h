@@ -48,7 +48,10 @@ struct DecodePlan {
 DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len, int dtype);
 size_t decode_workspace_bytes(int num_seqs, int n_heads, int max_slots);
 
-hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st);
+// single: the one-launch kernel (decode calls only, no workspace), else the
+// split workers and the merge kernel.
+hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, bool single,
+                               hipStream_t st);
 // Decode workers of a fused prefill launch: workgroups needed (sets
 // a.waves_per_group; 0 on a device error), and the merge that follows.
 int decode_worker_blocks(DecodeArgs& a);

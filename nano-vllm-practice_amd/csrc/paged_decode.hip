@@ -37,6 +37,70 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     decode_waves<E, NREP>(a, blockIdx.x);
 }
 
+// One-launch decode for calls of short contexts: one workgroup per (sequence,
+// KV head group), its four waves each taking a contiguous quarter of the
+// sequence's pages; the waves fold their states through LDS and write the
+// normalised rows, so no workspace and no merge launch are needed.  Decode
+// calls only (query row b, kv_lens[b] keys).
+template <typename E, int NREP>
+__global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) {
+    __shared__ float s_ml[4][NREP][2];
+    __shared__ float s_acc[4][NREP][kDimHead];
+    const int b = blockIdx.x, grp = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, rg = lane >> 4;
+    const int kvh = grp / a.head_groups;
+    const int h0 = kvh * a.n_rep + (grp - kvh * a.head_groups) * NREP;
+    const int kv_len = a.kv_lens[b];
+    const int npg = pages_of(kv_len);
+    const int per = (npg + 3) >> 2;
+    const int lp0 = min(npg, wave * per), lp1 = min(npg, lp0 + per);
+    float m[NREP], l[NREP], acc[NREP][8];
+    if (lp1 > lp0) {
+        decode_segment<E, NREP>(a, b, kv_len, lp0, lp1 - lp0, b, h0, (int64_t)kvh * a.pool_stride_head, m, l, acc);
+    } else {
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+            m[r] = kEmptyMax;
+            l[r] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[r][e] = 0.0f;
+        }
+    }
+    if (rg == 0) {
+#pragma unroll
+        for (int r = 0; r < NREP; ++r) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s_acc[wave][r][RowSlice<E>::dim(c, e)] = acc[r][e];
+            if (c == 0) {
+                s_ml[wave][r][0] = m[r];
+                s_ml[wave][r][1] = l[r];
+            }
+        }
+    }
+    __syncthreads();
+    char* out = reinterpret_cast<char*>(a.out);
+    for (int i = threadIdx.x; i < NREP * kDimHead; i += 256) {
+        const int r = i / kDimHead, d = i - r * kDimHead;
+        const int64_t o = (int64_t)(h0 + r) * a.out_stride_head + (int64_t)b * a.out_stride_seq + d;
+        if (npg == 0) {  // empty context: the reference stores its zero accumulator
+            store_elem<E>(out, o, 0.0f);
+            continue;
+        }
+        float M = kEmptyMax;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][r][0]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float f = fast_exp2(s_ml[w][r][0] - M);
+            L = fmaf(s_ml[w][r][1], f, L);
+            O = fmaf(s_acc[w][r][d], f, O);
+        }
+        store_elem<E>(out, o, O / L);
+    }
+}
+
 // Final softmax merge: one workgroup per (sequence, query head), one thread
 // per head dim.  Runs after the split kernel on the same stream.
 template <typename E>
@@ -134,7 +198,11 @@ hipError_t launch_paged_decode_merge(int dtype, const DecodeArgs& a, int num_seq
 }
 
 template <typename E, int NREP>
-static hipError_t launch_t(DecodeArgs a, int num_seqs, hipStream_t st) {
+static hipError_t launch_t(DecodeArgs a, int num_seqs, bool single, hipStream_t st) {
+    if (single) {
+        hipLaunchKernelGGL((paged_decode_single_kernel<E, NREP>), dim3(num_seqs, a.grid_heads), dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     const int grid = decode_worker_blocks(a);
     if (grid <= 0) return hipErrorInvalidDevice;
     hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), dim3(grid), dim3(256), 0, st, a);
@@ -144,24 +212,26 @@ static hipError_t launch_t(DecodeArgs a, int num_seqs, hipStream_t st) {
 }
 
 template <typename E>
-static hipError_t launch_e(const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st) {
+static hipError_t launch_e(const DecodeArgs& a, int nrep_tile, int num_seqs, bool single, hipStream_t st) {
     switch (nrep_tile) {
-        case 1: return launch_t<E, 1>(a, num_seqs, st);
-        case 2: return launch_t<E, 2>(a, num_seqs, st);
-        case 4: return launch_t<E, 4>(a, num_seqs, st);
+        case 1: return launch_t<E, 1>(a, num_seqs, single, st);
+        case 2: return launch_t<E, 2>(a, num_seqs, single, st);
+        case 4: return launch_t<E, 4>(a, num_seqs, single, st);
         case 8:
-            if constexpr (!std::is_same<E, F32>::value) return launch_t<E, 8>(a, num_seqs, st);
+            if constexpr (!std::is_same<E, F32>::value) return launch_t<E, 8>(a, num_seqs, single, st);
             return hipErrorInvalidValue;  // f32 plans stop at 4 heads per wave
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, hipStream_t st) {
+hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, int num_seqs, bool single,
+                               hipStream_t st) {
     if (num_seqs <= 0 || a.grid_heads <= 0) return hipSuccess;
+    if (single && a.cu_seqlens) return hipErrorInvalidValue;  // decode calls only
     switch (dtype) {
-        case kDtypeF32: return launch_e<F32>(a, nrep_tile, num_seqs, st);
-        case kDtypeF16: return launch_e<F16>(a, nrep_tile, num_seqs, st);
-        case kDtypeBF16: return launch_e<BF16>(a, nrep_tile, num_seqs, st);
+        case kDtypeF32: return launch_e<F32>(a, nrep_tile, num_seqs, single, st);
+        case kDtypeF16: return launch_e<F16>(a, nrep_tile, num_seqs, single, st);
+        case kDtypeBF16: return launch_e<BF16>(a, nrep_tile, num_seqs, single, st);
         default: return hipErrorInvalidValue;
     }
 }

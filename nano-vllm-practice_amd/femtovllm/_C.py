@@ -49,6 +49,8 @@ def _load() -> ctypes.CDLL:
         getattr(lib, name).argtypes = []
     lib.femto_paged_attention_gemv_workspace_size.restype = sz
     lib.femto_paged_attention_gemv_workspace_size.argtypes = [i, i, i]
+    lib.femto_attn_set_decode_single_max_kv.restype = i
+    lib.femto_attn_set_decode_single_max_kv.argtypes = [i]
     lib.femto_paged_attention_gemv.restype = i
     lib.femto_paged_attention_gemv.argtypes = [
         i, p, i64, i64, p, i64, i64, p, p, i64, i, i, i, i64, i64, i64, p, i, i64, p, i, i, i, p, sz, p,

@@ -216,6 +216,16 @@ def decode_bf16_qwen3_0p6b(poison=True) -> PagedWorkload:
     )
 
 
+def decode_bf16_short(poison=True) -> PagedWorkload:
+    """bf16 decode of short contexts, Qwen3-0.6B attention shape: B=64, L ~ U[64, 512], H=16, KVH=8."""
+    rng = np.random.default_rng(1006)
+    lens = [int(x) for x in rng.integers(64, 512, size=64, endpoint=True)]
+    return make_paged_workload(
+        "decode_bf16_qwen3_0.6b_b64_short", [(L - 1, 1) for L in lens], 16, 8,
+        seed=1006, poison=poison, rng=rng,
+    )
+
+
 def prefill_bf16_chunked(poison=True) -> PagedWorkload:
     """bf16 chunked prefill: 8 x 512-token chunks after prefixes U[0, 2048], H=16, KVH=8."""
     rng = np.random.default_rng(1003)

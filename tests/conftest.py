@@ -32,3 +32,16 @@ def ops(gpu):
     import femtovllm.ops
 
     return femtovllm.ops
+
+
+@pytest.fixture(params=["split", "one_launch"])
+def decode_path(request, gpu):
+    """Runs a decode test through both decode routes of the library: the split
+    workers + merge kernel, and the one-launch kernel (forced for every
+    length through femto_attn_set_decode_single_max_kv)."""
+    from femtovllm import _C
+
+    limit = -1 if request.param == "split" else (1 << 30)
+    prev = _C._lib.femto_attn_set_decode_single_max_kv(limit)
+    yield request.param
+    _C._lib.femto_attn_set_decode_single_max_kv(prev)

@@ -14,7 +14,7 @@ from femtovllm import workloads
 from femtovllm.metadata import build_varlen_metadata
 from helpers import assert_close, np32, np64, np_tables
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("decode_path")]
 
 
 def run_decode(ops, w, device, seqs=None):

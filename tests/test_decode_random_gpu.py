@@ -54,9 +54,9 @@ def test_generator_reaches_every_kind_of_batch():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("seed", range(48))
-def test_random_decode_batch(ops, gpu, seed):
+def test_random_decode_batch(ops, gpu, decode_path, seed):
     lens, H, KVH, dtype = random_batch(9000 + seed)
-    what = f"seed {9000 + seed}: H={H} KVH={KVH} {dtype} {len(lens)} seqs, max len {max(lens)}"
+    what = f"seed {9000 + seed} ({decode_path}): H={H} KVH={KVH} {dtype} {len(lens)} seqs, max len {max(lens)}"
     print(what, flush=True)
     # decode: the query token is the last of each context (a context of 0
     # keys is a chunk of one token with kv_len 0)

@@ -75,7 +75,17 @@ def test_noalloc_matches_workspace_entry_two_calls(gpu):
         assert_close(got, want, w.dtype, f"noalloc {w.name}")
 
 
-def test_noalloc_coarser_split_when_scratch_is_tight(gpu):
+@pytest.fixture
+def split_route(gpu):
+    """The split route (scratch in use) for every length, restored afterwards."""
+    from femtovllm import _C
+
+    prev = _C._lib.femto_attn_set_decode_single_max_kv(-1)
+    yield
+    _C._lib.femto_attn_set_decode_single_max_kv(prev)
+
+
+def test_noalloc_coarser_split_when_scratch_is_tight(gpu, split_route):
     """600 sequences x 32 heads: the default split needs more partial slots than
     the scratch holds, so sequences are cut into fewer slices; still within
     tolerance of the oracle and of the workspace entry point."""
@@ -96,8 +106,9 @@ def test_noalloc_coarser_split_when_scratch_is_tight(gpu):
     assert (got.float() - ref.float()).abs().max().item() <= 2e-2
 
 
-def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
-    """num_seqs * n_heads past the limit fails with a message and launches nothing."""
+def test_noalloc_rejects_calls_beyond_the_scratch(gpu, split_route):
+    """num_seqs * n_heads past the limit fails with a message and launches nothing
+    (on the split route; the one-launch route uses no scratch)."""
     from femtovllm import _C
 
     B = 40000
