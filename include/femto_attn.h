@@ -97,7 +97,11 @@ int femto_paged_attention_gemv(
  * (same results within rounding; bit-identical where the split is the
  * same).  All calls on one GPU share the array: calls that may overlap on
  * one GPU (different streams or threads) race and must be serialised by the
- * caller. */
+ * caller.  The first call on a device looks up the array's device address and
+ * the CU count (hipGetSymbolAddress, hipDeviceGetAttribute): make it outside
+ * graph capture; later calls only launch kernels and may be captured.  Every
+ * process that loads the library reserves the 64 MiB on each GPU it uses,
+ * whether or not it calls this entry point. */
 int femto_paged_attention_gemv_noalloc(
     int dtype,
     const void* q, int64_t q_stride_head, int64_t q_stride_seq,

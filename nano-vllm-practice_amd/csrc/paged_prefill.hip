@@ -324,6 +324,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             // Unsplit call, one sequence per thread: a single scan gives both
             // the work total and each sequence's first query tile.
             const int nt = tid < a.num_seqs && my_ql > 0 ? (my_ql + BT - 1) / BT : 0;
+            // beside decode workers with one-token sequences the copies are spread
+            if constexpr (FUSED) spread = __syncthreads_or(my_dec) != 0;
             int total;
             const int incl = block_incl_scan(nt, s_red, total);
             const int work = groups * total;

@@ -120,3 +120,38 @@ def test_noalloc_rejects_calls_beyond_the_scratch(gpu, split_route):
     assert rc == 1
     msg = _C._lib.femto_attn_last_error().decode()
     assert "scratch" in msg and "femto_paged_attention_gemv" in msg
+
+
+@pytest.mark.parametrize("lens", [(1500, 40, 3000, 700), (300, 17, 511, 2)], ids=["split_route", "one_launch_route"])
+def test_noalloc_under_graph_capture(gpu, lens):
+    """The allocation-free call captured in a HIP graph (after one call outside
+    capture, which sets up the device) and replayed with new q and kv_lens:
+    every replay matches the oracle and an eager call on the same inputs."""
+    from femtovllm import _C
+
+    w = workloads.make_paged_workload("graph", [(L - 1, 1) for L in lens], 16, 8, seed=73)
+    q, wd, meta = case(w, gpu)
+    kv_lens = meta.kv_lens.clone()
+    out = torch.empty_like(q)
+    rc, _ = gemv_noalloc(_C, q, wd.k_pool, wd.v_pool, meta.block_tables, kv_lens, meta.max_kv_len, out=out)
+    assert rc == 0, _C._lib.femto_attn_last_error().decode()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc, _ = gemv_noalloc(_C, q, wd.k_pool, wd.v_pool, meta.block_tables, kv_lens, meta.max_kv_len, out=out)
+    assert rc == 0, _C._lib.femto_attn_last_error().decode()
+    gen = torch.Generator().manual_seed(74)
+    rng = np.random.default_rng(74)
+    for rep in range(3):
+        q_new = torch.randn(q.shape, generator=gen).to(q.dtype)
+        new_lens = [int(rng.integers(1, L + 1)) for L in lens]
+        q.copy_(q_new.to(gpu))
+        kv_lens.copy_(torch.tensor(new_lens, dtype=torch.int32))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        eager = gemv_with_workspace(_C, q, wd.k_pool, wd.v_pool, meta.block_tables, kv_lens, meta.max_kv_len)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}: graph output differs from the eager call"
+        want = oa.paged_decode(np64(q_new), np32(w.k_pool), np32(w.v_pool), np_tables(meta), new_lens)
+        assert_close(out, want, w.dtype, f"graph replay {rep}, lens {new_lens}")
