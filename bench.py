@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill|long|mixed|flash|cache]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|decode_small|prefill|long|mixed|flash|cache]
                     [--no-cpu-baseline]
 
 Headline (``value``): paged decode attention, bf16, Qwen3-0.6B attention
@@ -63,7 +63,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", default="all",
-                    choices=["all", "decode", "prefill", "long", "mixed", "flash", "cache", "copy"])
+                    choices=["all", "decode", "decode_small", "prefill", "long", "mixed", "flash", "cache", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -301,6 +301,8 @@ def main():
             result["cpu_baseline"] = cpu_baseline_decode(w)
         del w
 
+    # ---------------- small decode calls (latency) ---------------------------
+    if want("decode_small"):
         # The reference's CPU-runnable case: fp32, 4 sequences, contexts
         # {17, 64, 200, 511}, and a 64-sequence step of short contexts; both
         # launch-bound (a few MB), so reported as latency.  Each is timed on
