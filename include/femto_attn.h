@@ -70,7 +70,9 @@ int femto_attn_set_decode_single_max_kv(int max_kv_len);
  * Replaces PagedAttentionGemvCuda (csrc/paged_attention/paged_attention_gemv.cu:223-308),
  * bound as _C.PagedAttentionGemvCuda (csrc/bindings.cpp:52-59, 94-97) and
  * called by femtovllm.ops.paged_attention_gemv (femtovllm/ops/__init__.py:82-107).
- * dtype: F32, F16 or BF16.  kv_len == 0 yields a zero row, as in the reference.
+ * dtype: F32, F16 or BF16.  head_dim <= 128 (the reference's TORCH_CHECK_LE,
+ * paged_attention_gemv.cu:256-257) in whole 16-byte chunks; scale 1/sqrt(head_dim).
+ * kv_len == 0 yields a zero row, as in the reference.
  * workspace may be NULL (0 bytes) when max_kv_len is within the one-launch
  * limit of femto_attn_set_decode_single_max_kv. */
 int femto_paged_attention_gemv(

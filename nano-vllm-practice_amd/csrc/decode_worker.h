@@ -20,6 +20,15 @@ struct RowSlice<BF16> {
     __device__ __forceinline__ void load(const char* row, int c) { w = ld16(row + 16 * c); }
     __device__ __forceinline__ void stream(const char* row, int c) { w = ld16_nt(row + 16 * c); }
     __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
+    // head_dim D < 128: chunks at or past D are not read and hold zeros
+    __device__ __forceinline__ void load_d(const char* row, int c, int D) {
+        if (8 * c < D) load(row, c);
+        else zero();
+    }
+    __device__ __forceinline__ void stream_d(const char* row, int c, int D) {
+        if (8 * c < D) stream(row, c);
+        else zero();
+    }
     __device__ __forceinline__ void to_float(float f[8]) const { unpack8(BF16{}, w, f); }
     // sum over the 8 dims of this * o, products exact, fp32 accumulation
     __device__ __forceinline__ float dot(const RowSlice& o) const {
@@ -40,6 +49,14 @@ struct RowSlice<F16> {
     __device__ __forceinline__ void load(const char* row, int c) { w = ld16(row + 16 * c); }
     __device__ __forceinline__ void stream(const char* row, int c) { w = ld16_nt(row + 16 * c); }
     __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
+    __device__ __forceinline__ void load_d(const char* row, int c, int D) {
+        if (8 * c < D) load(row, c);
+        else zero();
+    }
+    __device__ __forceinline__ void stream_d(const char* row, int c, int D) {
+        if (8 * c < D) stream(row, c);
+        else zero();
+    }
     __device__ __forceinline__ void to_float(float f[8]) const { unpack8(F16{}, w, f); }
     __device__ __forceinline__ float dot(const RowSlice& o) const {
         typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -69,6 +86,14 @@ struct RowSlice<F32> {
     __device__ __forceinline__ void zero() {
         a = u32x4{0, 0, 0, 0};
         b = u32x4{0, 0, 0, 0};
+    }
+    __device__ __forceinline__ void load_d(const char* row, int c, int D) {
+        a = 4 * c < D ? ld16(row + 16 * c) : u32x4{0, 0, 0, 0};
+        b = 64 + 4 * c < D ? ld16(row + 256 + 16 * c) : u32x4{0, 0, 0, 0};
+    }
+    __device__ __forceinline__ void stream_d(const char* row, int c, int D) {
+        a = 4 * c < D ? ld16_nt(row + 16 * c) : u32x4{0, 0, 0, 0};
+        b = 64 + 4 * c < D ? ld16_nt(row + 256 + 16 * c) : u32x4{0, 0, 0, 0};
     }
     __device__ __forceinline__ void to_float(float f[8]) const {
 #pragma unroll
@@ -221,7 +246,10 @@ __device__ __forceinline__ int decode_len(const DecodeArgs& a, int b) {
 // lane's dims.  On return every lane holds the state of the whole wave for
 // its dims (lane & 15).  Used by the split workers (one segment of a slice)
 // and by the one-launch kernel (a quarter of a sequence per wave).
-template <typename E, int NREP>
+//
+// FULL: head_dim == 128 (every lane reads its 8 dims); else a.head_dim < 128
+// and lanes read only the dims below it (the rest are zeros).
+template <typename E, int NREP, bool FULL = true>
 __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int kv_len, int lp0, int n, int qrow,
                                                int h0, int64_t head_off, float (&m)[NREP], float (&l)[NREP],
                                                float (&acc)[NREP][8]) {
@@ -235,7 +263,11 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int k
     RowSlice<E> qs[NREP];
 #pragma unroll
     for (int r = 0; r < NREP; ++r)
-        qs[r].load(qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)qrow * a.q_stride_seq) * EB, c);
+    {
+        const char* qr = qbase + ((int64_t)(h0 + r) * a.q_stride_head + (int64_t)qrow * a.q_stride_seq) * EB;
+        if constexpr (FULL) qs[r].load(qr, c);
+        else qs[r].load_d(qr, c, a.head_dim);
+    }
 #pragma unroll
     for (int r = 0; r < NREP; ++r) {
         m[r] = kEmptyMax;
@@ -264,8 +296,13 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int k
         for (int j = 0; j < 4; ++j) {
             const int row = min(rg + 4 * j, last_row);
             const int64_t off = page_off + (int64_t)row * a.pool_stride_row * EB;
-            pr.k[j].stream(kpool + off, c);
-            pr.v[j].stream(vpool + off, c);
+            if constexpr (FULL) {
+                pr.k[j].stream(kpool + off, c);
+                pr.v[j].stream(vpool + off, c);
+            } else {
+                pr.k[j].stream_d(kpool + off, c, a.head_dim);
+                pr.v[j].stream_d(vpool + off, c, a.head_dim);
+            }
         }
     };
     auto consume = [&](int i, PageRegs<E>& pr, bool blk_ok) {
@@ -395,7 +432,7 @@ __device__ __forceinline__ void decode_segment(const DecodeArgs& a, int b, int k
 // The waves of workgroup `block` (4 per workgroup, no barriers: a wave may
 // return on its own); used by the decode kernel and by the fused prefill
 // launch, whose first workgroups are decode workers.
-template <typename E, int NREP>
+template <typename E, int NREP, bool FULL = true>
 __device__ __forceinline__ void decode_waves(const DecodeArgs& a, int block) {
     const int lane = threadIdx.x & 63;
     const int gw = block * 4 + (threadIdx.x >> 6);
@@ -472,7 +509,7 @@ __device__ __forceinline__ void decode_waves(const DecodeArgs& a, int block) {
 
         const int qrow = a.cu_seqlens ? a.cu_seqlens[b] : b;
         float m[NREP], l[NREP], acc[NREP][8];
-        decode_segment<E, NREP>(a, b, kv_len, lp0, n, qrow, h0, head_off, m, l, acc);
+        decode_segment<E, NREP, FULL>(a, b, kv_len, lp0, n, qrow, h0, head_off, m, l, acc);
 
         // Partial state of this segment.
         const int slot = wi - S / C;

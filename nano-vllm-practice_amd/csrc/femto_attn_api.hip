@@ -58,11 +58,20 @@ int check_paged_common(const char* fn, int dtype, const void* q, const void* out
                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
                               int head_dim, int64_t ps0, int64_t ps1, int64_t ps2, int n_heads,
                               int64_t q_s0, int64_t q_s1, const int32_t* tables, int num_pages_per_seq,
-                              int64_t table_stride) {
+                              int64_t table_stride, bool any_head_dim = false) {
     std::string f(fn);
-    if (head_dim != femto::kDimHead)
+    if (any_head_dim) {
+        // decode: head_dim <= 128 as the reference checks
+        // (paged_attention_gemv.cu:256-257), in whole 16-byte chunks
+        if (head_dim <= 0 || head_dim > femto::kDimHead || (head_dim * elem_bytes(dtype)) % 16 != 0)
+            return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be at most " + std::to_string(femto::kDimHead) +
+                                                   " and a multiple of 16 bytes (" +
+                                                   std::to_string(16 / elem_bytes(dtype)) + " elements), got " +
+                                                   std::to_string(head_dim));
+    } else if (head_dim != femto::kDimHead) {
         return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be " + std::to_string(femto::kDimHead) + ", got " +
                                                std::to_string(head_dim));
+    }
     if (block_size != femto::kPage)
         return fail(FEMTO_ERR_INVALID, f + ": block_size must be " + std::to_string(femto::kPage) + ", got " +
                                            std::to_string(block_size));
@@ -176,6 +185,7 @@ DecodeArgs decode_args(const DecodePlan& plan, const void* q, int64_t q_stride_h
     a.grid_heads = n_heads / plan.nrep_tile;
     a.min_chunk_pages = plan.min_chunk_pages;
     a.max_slots = plan.max_slots;
+    a.head_dim = head_dim;
     a.scale_log2 = ::scale_log2(head_dim);
     const size_t slots = (size_t)num_seqs * n_heads * plan.max_slots;
     a.part_acc = static_cast<float*>(workspace);
@@ -218,7 +228,7 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
     if (!kv_lens) return fail(FEMTO_ERR_INVALID, fn + ": null kv_lens");
     int rc = check_paged_common(fn_name, dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
                                 block_size, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, n_heads,
-                                q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride);
+                                q_stride_head, q_stride_seq, kv_page_tables, num_pages_per_seq, table_stride, true);
     if (rc != FEMTO_OK) return rc;
 
     femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len, dtype);

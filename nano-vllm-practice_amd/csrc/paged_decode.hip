@@ -32,9 +32,9 @@
 
 namespace femto {
 
-template <typename E, int NREP>
+template <typename E, int NREP, bool FULL>
 __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
-    decode_waves<E, NREP>(a, blockIdx.x);
+    decode_waves<E, NREP, FULL>(a, blockIdx.x);
 }
 
 // One-launch decode for calls of short contexts: one workgroup per (sequence,
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
 // sequence's pages; the waves fold their states through LDS and write the
 // normalised rows, so no workspace and no merge launch are needed.  Decode
 // calls only (query row b, kv_lens[b] keys).
-template <typename E, int NREP>
+template <typename E, int NREP, bool FULL>
 __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) {
     __shared__ float s_ml[4][NREP][2];
     __shared__ float s_acc[4][NREP][kDimHead];
@@ -57,7 +57,8 @@ __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) 
     const int lp0 = min(npg, wave * per), lp1 = min(npg, lp0 + per);
     float m[NREP], l[NREP], acc[NREP][8];
     if (lp1 > lp0) {
-        decode_segment<E, NREP>(a, b, kv_len, lp0, lp1 - lp0, b, h0, (int64_t)kvh * a.pool_stride_head, m, l, acc);
+        decode_segment<E, NREP, FULL>(a, b, kv_len, lp0, lp1 - lp0, b, h0, (int64_t)kvh * a.pool_stride_head, m, l,
+                                      acc);
     } else {
 #pragma unroll
         for (int r = 0; r < NREP; ++r) {
@@ -82,6 +83,7 @@ __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) 
     char* out = reinterpret_cast<char*>(a.out);
     for (int i = threadIdx.x; i < NREP * kDimHead; i += 256) {
         const int r = i / kDimHead, d = i - r * kDimHead;
+        if (!FULL && d >= a.head_dim) continue;
         const int64_t o = (int64_t)(h0 + r) * a.out_stride_head + (int64_t)b * a.out_stride_seq + d;
         if (npg == 0) {  // empty context: the reference stores its zero accumulator
             store_elem<E>(out, o, 0.0f);
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
         // and its zero accumulator is stored (paged_attention_gemv.cu:203-218).
         // Decode row of a prefill call: 0 / 0, NaN, as the prefill kernels
         // give for a row with no visible key.
-        store_elem<E>(out, o, a.cu_seqlens ? __builtin_nanf("") : 0.0f);
+        if (t < a.head_dim) store_elem<E>(out, o, a.cu_seqlens ? __builtin_nanf("") : 0.0f);
         return;
     }
     const int count = count_ld;
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
         L = fmaf(s_lv[i], wi, L);
         O = fmaf(src[(int64_t)i * kDimHead], wi, O);
     }
-    store_elem<E>(out, o, O / L);
+    if (t < a.head_dim) store_elem<E>(out, o, O / L);
 }
 
 // One wave per SIMD (4 per CU), each with three pages of K and V in flight
@@ -197,28 +199,29 @@ hipError_t launch_paged_decode_merge(int dtype, const DecodeArgs& a, int num_seq
     }
 }
 
-template <typename E, int NREP>
+template <typename E, int NREP, bool FULL>
 static hipError_t launch_t(DecodeArgs a, int num_seqs, bool single, hipStream_t st) {
     if (single) {
-        hipLaunchKernelGGL((paged_decode_single_kernel<E, NREP>), dim3(num_seqs, a.grid_heads), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((paged_decode_single_kernel<E, NREP, FULL>), dim3(num_seqs, a.grid_heads), dim3(256), 0, st,
+                           a);
         return hipGetLastError();
     }
     const int grid = decode_worker_blocks(a);
     if (grid <= 0) return hipErrorInvalidDevice;
-    hipLaunchKernelGGL((paged_decode_kernel<E, NREP>), dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((paged_decode_kernel<E, NREP, FULL>), dim3(grid), dim3(256), 0, st, a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_merge_t<E>(a, num_seqs, st);
 }
 
-template <typename E>
+template <typename E, bool FULL>
 static hipError_t launch_e(const DecodeArgs& a, int nrep_tile, int num_seqs, bool single, hipStream_t st) {
     switch (nrep_tile) {
-        case 1: return launch_t<E, 1>(a, num_seqs, single, st);
-        case 2: return launch_t<E, 2>(a, num_seqs, single, st);
-        case 4: return launch_t<E, 4>(a, num_seqs, single, st);
+        case 1: return launch_t<E, 1, FULL>(a, num_seqs, single, st);
+        case 2: return launch_t<E, 2, FULL>(a, num_seqs, single, st);
+        case 4: return launch_t<E, 4, FULL>(a, num_seqs, single, st);
         case 8:
-            if constexpr (!std::is_same<E, F32>::value) return launch_t<E, 8>(a, num_seqs, single, st);
+            if constexpr (!std::is_same<E, F32>::value) return launch_t<E, 8, FULL>(a, num_seqs, single, st);
             return hipErrorInvalidValue;  // f32 plans stop at 4 heads per wave
         default: return hipErrorInvalidValue;
     }
@@ -228,10 +231,15 @@ hipError_t launch_paged_decode(int dtype, const DecodeArgs& a, int nrep_tile, in
                                hipStream_t st) {
     if (num_seqs <= 0 || a.grid_heads <= 0) return hipSuccess;
     if (single && a.cu_seqlens) return hipErrorInvalidValue;  // decode calls only
+    if (a.head_dim <= 0 || a.head_dim > kDimHead) return hipErrorInvalidValue;
+    const bool full = a.head_dim == kDimHead;
     switch (dtype) {
-        case kDtypeF32: return launch_e<F32>(a, nrep_tile, num_seqs, single, st);
-        case kDtypeF16: return launch_e<F16>(a, nrep_tile, num_seqs, single, st);
-        case kDtypeBF16: return launch_e<BF16>(a, nrep_tile, num_seqs, single, st);
+        case kDtypeF32: return full ? launch_e<F32, true>(a, nrep_tile, num_seqs, single, st)
+                                    : launch_e<F32, false>(a, nrep_tile, num_seqs, single, st);
+        case kDtypeF16: return full ? launch_e<F16, true>(a, nrep_tile, num_seqs, single, st)
+                                    : launch_e<F16, false>(a, nrep_tile, num_seqs, single, st);
+        case kDtypeBF16: return full ? launch_e<BF16, true>(a, nrep_tile, num_seqs, single, st)
+                                     : launch_e<BF16, false>(a, nrep_tile, num_seqs, single, st);
         default: return hipErrorInvalidValue;
     }
 }

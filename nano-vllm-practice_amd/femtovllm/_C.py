@@ -155,7 +155,7 @@ def _prefill_workspace(device: torch.device, num_seqs: int, num_tokens: int, max
     return _cached_workspace(_prefill_workspaces, device, nbytes, zero=True)
 
 
-def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q):
+def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q, any_head_dim=False):
     for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
         _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
     if require_contiguous_q:
@@ -174,9 +174,16 @@ def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q):
     for name, t in (("kv_page_tables", tables), ("kv_lens", kv_lens)):
         _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
     _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}, got {k_pool.size(2)}")
-    # The reference accepts head_dim <= 128 (paged_attention_gemv.cu TORCH_CHECK_LE(dim_d, kDimHead)); the
-    # MFMA and wave tilings here are built for exactly 128, the head_dim of every model the engine runs.
-    _check(q.size(-1) == kDimHead, f"{fn}: head_dim must be {kDimHead}, got {q.size(-1)}")
+    if any_head_dim:
+        # Decode: head_dim <= 128, TORCH_CHECK_LE(dim_d, kDimHead) (paged_attention_gemv.cu:256-257), in
+        # whole 16-byte chunks (the wave loads rows 16 bytes per lane).
+        _check(q.size(-1) <= kDimHead, f"{fn}: head_dim must be <= {kDimHead}, got {q.size(-1)}")
+        _check((q.size(-1) * q.element_size()) % 16 == 0,
+               f"{fn}: head_dim must be a multiple of 16 bytes ({16 // q.element_size()} elements), got {q.size(-1)}")
+    else:
+        # Prefill: the MFMA tiling is built for exactly 128, the head_dim of every model the engine runs
+        # (the reference's checks accept <= 128, paged_attention_gemm.cu:348).
+        _check(q.size(-1) == kDimHead, f"{fn}: head_dim must be {kDimHead}, got {q.size(-1)}")
     _check(q.size(0) % k_pool.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
 
 
@@ -186,7 +193,7 @@ def _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len
     ``kMaxKVLenNonSplit`` check (paged_attention_gemv.cu:271-274); ``None``
     lifts it, since the kernel splits contexts of any length over waves."""
     fn = "PagedAttentionGemvCuda"
-    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q)
+    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q, any_head_dim=True)
     n_heads, num_seqs, dim = q.shape
     _check(num_seqs == kv_page_tables.size(0), f"{fn}: q.size(1) must equal kv_page_tables.size(0)")
     _check(num_seqs == kv_lens.size(0), f"{fn}: q.size(1) must equal kv_lens.size(0)")

@@ -75,7 +75,10 @@ def _gemv(C, **kw):
 
 def test_gemv_validation_errors(C):
     last = lambda: C._lib.femto_attn_last_error().decode()
-    assert _gemv(C, d=64) == 2 and "head_dim must be 128" in last()
+    # decode takes head_dim <= 128 in 16-byte chunks (the reference's TORCH_CHECK_LE)
+    assert _gemv(C, d=136) == 2 and "head_dim must be at most 128" in last()
+    assert _gemv(C, d=100) == 2 and "multiple of 16 bytes" in last()
+    assert _gemv(C, d=0) == 2 and "head_dim" in last()
     assert _gemv(C, bs=32) == 1 and "block_size must be 16" in last()
     assert _gemv(C, h=12) == 1 and "multiple of n_kv_heads" in last()
     assert _gemv(C, dtype=7) == 2

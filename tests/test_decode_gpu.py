@@ -178,3 +178,37 @@ def test_decode_errors(ops, gpu):
                                  meta.max_kv_len)
     with pytest.raises(RuntimeError):
         ops.paged_attention_gemv(q.to(gpu), wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens, 8193)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.bfloat16, 96), (torch.float16, 8),
+                                     (torch.float16, 120), (torch.float32, 64), (torch.float32, 4),
+                                     (torch.float32, 100)])
+def test_decode_head_dim_below_128(ops, gpu, dtype, D):
+    """head_dim <= 128 as the reference's decode accepts (TORCH_CHECK_LE(dim_d, kDimHead),
+    csrc/paged_attention/paged_attention_gemv.cu:256-257): rows of D elements, scale
+    1/sqrt(D); NaN-poisoned tails and unused blocks sit right after the rows read."""
+    rng = np.random.default_rng(D)
+    lens = [int(x) for x in rng.integers(1, 1500, size=6)] + [16, 1]
+    w = workloads.make_paged_workload("head_dim", [(L - 1, 1) for L in lens], 16, 4, head_dim=D, dtype=dtype,
+                                      seed=D + 5)
+    from femtovllm import _C
+
+    q, meta = w.gemv_call(device=gpu)
+    wd = w.to(gpu)
+    out = _C._paged_attention_gemv(q.to(gpu), wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
+                                   meta.max_kv_len)
+    torch.cuda.synchronize()
+    assert out.shape == (16, len(lens), D)
+    assert_close(out, oracle_decode(w, q, meta), dtype, f"decode head_dim {D} {dtype}")
+
+
+def test_decode_head_dim_errors(ops, gpu):
+    from femtovllm import _C
+
+    for D, dtype in ((136, torch.bfloat16), (100, torch.bfloat16), (6, torch.float32)):
+        w = workloads.make_paged_workload("hd_err", [(30, 1)], 4, 2, head_dim=D, dtype=dtype, seed=1)
+        q, meta = w.gemv_call(device=gpu)
+        wd = w.to(gpu)
+        with pytest.raises(RuntimeError, match="head_dim"):
+            _C._paged_attention_gemv(q.to(gpu), wd.k_pool, wd.v_pool, meta.block_tables, meta.kv_lens,
+                                     meta.max_kv_len)
