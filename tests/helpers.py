@@ -14,6 +14,16 @@ import torch
 # (csrc/flash_attention/test_flash_attention.py:51).
 ATOL = {torch.float32: 1e-4, torch.bfloat16: 1e-2, torch.float16: 1e-3}
 RTOL = {torch.float32: 0.0, torch.bfloat16: 0.0, torch.float16: 1e-3}
+# The max-abs bound holds for the value before its final rounding to the
+# output type; that rounding adds half an ulp at |want| (0.0078 for a bf16
+# output in [2, 4), where the grid is 2^-6 wide).  Without it no kernel that
+# stores bf16 meets 1e-2 on rows of a few visible keys with |out| >= 2: the
+# reference's own arithmetic (fp32 softmax, weights cast to bf16 before P.V,
+# bf16 store; femtovllm/ops/triton/paged_attention/paged_attention_gemm.py:
+# 122-160, restated in oracle/ref_arith.py) exceeds a plain 1e-2 against the
+# float64 oracle there and stays within 1e-2 + half an ulp
+# (tests/test_oracle.py::test_ref_arith_needs_the_output_rounding_allowance).
+# Below |want| = 1.28 a bf16 half ulp is at most 2^-9 x 1.28 = 0.0025.
 
 # Scale-aware bound, checked beside the max-abs one.  Attention outputs
 # shrink with context length (N(0,1) inputs give an output RMS of about
@@ -80,7 +90,7 @@ def assert_close(got: torch.Tensor, want: np.ndarray, dtype: torch.dtype, what: 
     assert np.array_equal(nan_g, nan_w), f"{what}: NaN pattern differs ({nan_g.sum()} vs {nan_w.sum()})"
     ok = ~nan_w
     err = np.abs(g[ok] - w[ok])
-    tol = ATOL[dtype] + RTOL[dtype] * np.abs(w[ok])
+    tol = ATOL[dtype] + RTOL[dtype] * np.abs(w[ok]) + half_ulp(np.abs(w[ok]), dtype)
     worst = float(err.max()) if err.size else 0.0
     rbo = rb[ok]
     ratio = float((err / np.where(rbo > 0, rbo, np.inf)).max()) if err.size else 0.0
@@ -95,7 +105,8 @@ def assert_close(got: torch.Tensor, want: np.ndarray, dtype: torch.dtype, what: 
     if log:
         with open(log, "a") as f:
             f.write(json.dumps(rec) + "\n")
-    assert np.all(err <= tol), f"{what}: max abs err {worst:.3e} exceeds tolerance (atol {ATOL[dtype]}, rtol {RTOL[dtype]})"
+    assert np.all(err <= tol), (f"{what}: max abs err {worst:.3e} exceeds tolerance (atol {ATOL[dtype]}, "
+                                f"rtol {RTOL[dtype]}, + half an output ulp)")
     assert ratio <= 1.0, (f"{what}: error reaches {ratio:.2f}x the per-row bound "
                           f"({ROW_REL[dtype]:.2e} x max|row| + half ulp); relative RMS error {rel_rms:.2e}")
     return worst

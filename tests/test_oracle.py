@@ -510,3 +510,59 @@ def test_row_bound_has_power_at_131072_keys():
         assert np.abs(np64(scaled) - want).max() <= 1e-2  # max-abs alone would pass
         with pytest.raises(AssertionError, match="per-row bound"):
             assert_close(scaled, want, torch.bfloat16, f"oracle x {factor}")
+
+
+# ---------------------------------------------------------------------------
+# The reference kernel's own precision (oracle/ref_arith.py) and the max-abs
+# bound of the parity helper.
+# ---------------------------------------------------------------------------
+
+
+def _bf16_values(rng, shape, sigma=1.0):
+    """Random values that are exact bf16 numbers, as float32."""
+    from oracle.ref_arith import bf16_round
+
+    return bf16_round(rng.standard_normal(shape) * sigma)
+
+
+def test_ref_arith_equal_scores_give_the_rounded_mean():
+    """q == 0: every weight is exp(0) = 1 (exact in bf16), so the reference's
+    arithmetic returns the bf16 rounding of the exact mean of the V rows
+    (2 and 4 keys: sums and the division are exact in fp32)."""
+    from oracle.ref_arith import bf16_round, prefill_row_bf16
+
+    rng = np.random.default_rng(5)
+    for L in (1, 2, 4):
+        k = _bf16_values(rng, (L, 128))
+        v = _bf16_values(rng, (L, 128), 3.0)
+        got = prefill_row_bf16(np.zeros(128, np.float32), k, v, oa.softmax_scale(128))
+        want = bf16_round(v.astype(np.float64).mean(axis=0))
+        assert np.array_equal(got, want)
+
+
+def test_ref_arith_needs_the_output_rounding_allowance():
+    """The reference's arithmetic (fp32 softmax, weights cast to bf16 before
+    P.V, bf16 output) on rows of a few visible keys with outputs of magnitude
+    2-8: against the float64 oracle it exceeds a plain max-abs 1e-2 on some
+    rows (the bf16 grid there is 2^-6 to 2^-5 wide), and it always stays
+    within 1e-2 plus half a bf16 ulp of the exact value, the bound the parity
+    helper uses."""
+    from helpers import half_ulp
+    from oracle.ref_arith import prefill_row_bf16
+
+    rng = np.random.default_rng(11)
+    scale = oa.softmax_scale(128)
+    over, worst_excess = 0, 0.0
+    for _ in range(3000):
+        L = int(rng.integers(1, 4))
+        q = _bf16_values(rng, (128,))
+        k = _bf16_values(rng, (L, 128))
+        v = _bf16_values(rng, (L, 128), 3.0)
+        got = prefill_row_bf16(q, k, v, scale).astype(np.float64)
+        want = oa._softmax_attend(q[None].astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                                  np.ones((1, L), bool), scale)[0]
+        err = np.abs(got - want)
+        over += int(np.any(err > 1e-2))
+        worst_excess = max(worst_excess, float((err - 1e-2 - half_ulp(np.abs(want), torch.bfloat16)).max()))
+    assert over > 0
+    assert worst_excess <= 0.0
