@@ -14,7 +14,7 @@
  * same thread).
  *
  * Layouts (all strides in elements, innermost dimension contiguous):
- *   paged pool  (num_blocks, n_kv_heads, block_size = 16, head_dim = 128)
+ *   paged pool  (num_blocks, n_kv_heads, block_size = 16, head_dim <= 128)
  *   block table (num_seqs, num_pages_per_seq) int32, -1 padded
  *   decode q/out  (n_heads, num_seqs, head_dim)
  *   prefill q/out (n_heads, num_tokens, head_dim), sequences by cu_seqlens
@@ -123,8 +123,10 @@ int femto_paged_attention_gemv_noalloc(
  * (femtovllm/ops/triton/paged_attention/paged_attention_gemm.py:165-235),
  * bound as _C.PagedAttentionGemmCuda (csrc/bindings.cpp:41-50, 90-93) and
  * called by femtovllm.ops.paged_attention_gemm (femtovllm/ops/__init__.py:110-156).
- * dtype: F16 or BF16 (the reference kernels reject F32 too).  A row with
- * no visible key (kv_len == 0) is NaN, as in the reference.
+ * dtype: F16 or BF16 (the reference kernels reject F32 too).  head_dim <=
+ * 128 as the reference checks (paged_attention_gemm.cu:347-348), a multiple
+ * of 16 (smaller ones run at the speed of 128); scale 1/sqrt(head_dim).  A
+ * row with no visible key (kv_len == 0) is NaN, as in the reference.
  * max_q_len: the longest sequence's token count, as the reference binding
  * takes it; it only bounds how many sequences may have exactly one token.
  * workspace may be NULL.  With a workspace of at least

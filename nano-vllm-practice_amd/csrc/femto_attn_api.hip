@@ -58,20 +58,18 @@ int check_paged_common(const char* fn, int dtype, const void* q, const void* out
                               const void* v_pool, int64_t num_blocks, int n_kv_heads, int block_size,
                               int head_dim, int64_t ps0, int64_t ps1, int64_t ps2, int n_heads,
                               int64_t q_s0, int64_t q_s1, const int32_t* tables, int num_pages_per_seq,
-                              int64_t table_stride, bool any_head_dim = false) {
+                              int64_t table_stride, bool decode) {
     std::string f(fn);
-    if (any_head_dim) {
-        // decode: head_dim <= 128 as the reference checks
-        // (paged_attention_gemv.cu:256-257), in whole 16-byte chunks
-        if (head_dim <= 0 || head_dim > femto::kDimHead || (head_dim * elem_bytes(dtype)) % 16 != 0)
-            return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be at most " + std::to_string(femto::kDimHead) +
-                                                   " and a multiple of 16 bytes (" +
-                                                   std::to_string(16 / elem_bytes(dtype)) + " elements), got " +
-                                                   std::to_string(head_dim));
-    } else if (head_dim != femto::kDimHead) {
-        return fail(FEMTO_ERR_UNSUPPORTED, f + ": head_dim must be " + std::to_string(femto::kDimHead) + ", got " +
-                                               std::to_string(head_dim));
-    }
+    // head_dim <= 128 as the reference checks (decode:
+    // paged_attention_gemv.cu:256-257; prefill: paged_attention_gemm.cu:347-348),
+    // in whole 16-byte chunks for decode (a lane loads 16-byte pieces of a
+    // row) and in multiples of 16 for prefill (one score MFMA step).
+    const int unit = decode ? 16 / elem_bytes(dtype) : 16;
+    if (head_dim <= 0 || head_dim > femto::kDimHead || head_dim % unit != 0)
+        return fail(FEMTO_ERR_UNSUPPORTED,
+                    f + ": head_dim must be at most " + std::to_string(femto::kDimHead) + " and a multiple of " +
+                        (decode ? "16 bytes (" + std::to_string(unit) + " elements)" : std::string("16")) +
+                        ", got " + std::to_string(head_dim));
     if (block_size != femto::kPage)
         return fail(FEMTO_ERR_INVALID, f + ": block_size must be " + std::to_string(femto::kPage) + ", got " +
                                            std::to_string(block_size));
@@ -376,7 +374,7 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: null cu_seqlens / kv_lens / positions");
     int rc = check_paged_common("paged_attention_gemm", dtype, q, out, k_pool, v_pool, num_blocks, n_kv_heads,
                                 block_size, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, n_heads,
-                                q_stride_head, q_stride_token, kv_page_tables, num_pages_per_seq, table_stride);
+                                q_stride_head, q_stride_token, kv_page_tables, num_pages_per_seq, table_stride, false);
     if (rc != FEMTO_OK) return rc;
     if (out_stride_head % 4 || out_stride_token % 4)
         return fail(FEMTO_ERR_INVALID, "paged_attention_gemm: out strides must be multiples of 8 bytes");
@@ -408,6 +406,7 @@ int femto_paged_attention_gemm(int dtype, const void* q, int64_t q_stride_head, 
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
     a.n_rep = n_heads / n_kv_heads;
+    a.head_dim = head_dim;
     a.scale_log2 = scale_log2(head_dim);
     hipStream_t st = static_cast<hipStream_t>(stream);
     int decode_rows = 0;
@@ -685,6 +684,7 @@ int femto_flash_attention(int dtype, const void* q, int64_t q_stride_batch, int6
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
     a.n_rep = n_heads / n_kv_heads;
+    a.head_dim = head_dim;
     a.scale_log2 = scale_log2(head_dim);
     return hip_status(femto::launch_dense_attention(dtype, a, static_cast<hipStream_t>(stream)),
                       "flash_attention launch");

@@ -81,6 +81,7 @@ struct PrefillArgs {
     int n_heads, n_kv_heads, n_rep, head_groups;
     int tiles_per_group;  // upper bound on workgroups per (kv head, head group)
     int total_work;       // tiles_per_group * n_kv_heads * head_groups (grid size)
+    int head_dim;         // 128; paged calls also a smaller multiple of 16
     float scale_log2;
     // Key split of long query tiles (paged only; part == nullptr: none).
     float* part;          // one partial slot of kPartSlotBytes per resident workgroup

@@ -227,7 +227,15 @@ __device__ __forceinline__ int serpentine(int k, int n, int cus) {
     return round * cus + (in_round - 1 - pos);
 }
 
-template <typename E, int G, bool PAGED, bool FUSED>
+// FULLD: head_dim == 128.  Else (paged calls only) head_dim is a smaller
+// multiple of 16 and the tile loop is the same code: K and V rows keep
+// their 256-byte LDS slots, and lanes whose 16-byte chunk lies at or past
+// head_dim copy chunk 0 of the same row instead (in bounds, finite for
+// finite pools); Q is zero past head_dim, so those K dims add nothing to the
+// scores; the V dims past head_dim only reach output dims that are not
+// stored.  The MFMAs past head_dim are spent for nothing: such calls run
+// at the speed of head_dim 128.
+template <typename E, int G, bool PAGED, bool FUSED, bool FULLD = true>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_mfma_kernel(PrefillArgs a) {
     constexpr int EB = 2;
     constexpr int BT = 32 * (4 / G);
@@ -252,7 +260,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         // the decode kernel would use for this head ratio); they are
         // dispatched first, one per CU, and the tiles fill the other slots.
         if (lin < a.decode_blocks) {
-            decode_waves<E, G>(a.dec, lin);
+            decode_waves<E, G, FULLD>(a.dec, lin);
             return;
         }
         lin -= a.decode_blocks;  // a multiple of 8: the XCD of a tile is unchanged
@@ -474,11 +482,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int rs_k = (int)a.k_stride2 * EB, rs_v = (int)a.v_stride2 * EB;
     int koff[4], voff[4];
     uint32_t kfull[4], vfull[4];
+    const int nchunks = FULLD ? 16 : a.head_dim / 8;  // 16-byte chunks per row
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int r = 4 * j + lrow;
-        koff[j] = ((lpos ^ swz_k(r)) << 4);
-        voff[j] = ((lpos ^ swz_v(r)) << 4);
+        const int ck = lpos ^ swz_k(r), cv = lpos ^ swz_v(r);
+        koff[j] = ((FULLD || ck < nchunks) ? ck : 0) << 4;
+        voff[j] = ((FULLD || cv < nchunks) ? cv : 0) << 4;
         kfull[j] = (uint32_t)(r * rs_k + koff[j]);
         vfull[j] = (uint32_t)(r * rs_v + voff[j]);
     }
@@ -614,7 +624,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const char* qrow = reinterpret_cast<const char*>(a.q) +
                            ((int64_t)b * a.q_stride_batch + (int64_t)h * a.q_stride_head + (int64_t)t * a.q_stride_token) * EB;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) qreg[kk] = qvalid ? ld16(qrow + (16 * kk + 8 * h2) * EB) : u32x4{0, 0, 0, 0};
+        for (int kk = 0; kk < 8; ++kk)
+            qreg[kk] = (qvalid && (FULLD || 16 * kk < a.head_dim)) ? ld16(qrow + (16 * kk + 8 * h2) * EB)
+                                                                  : u32x4{0, 0, 0, 0};
     }
 
     // Per-lane constant parts of the LDS operand addresses.
@@ -967,6 +979,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int d0 = 32 * dt + 8 * g + 4 * h2;
+                if (!FULLD && d0 >= a.head_dim) continue;  // head_dim is a multiple of 16: d0 + 4 <= head_dim
                 const u32x2 v = pack4(E{}, oacc[dt][4 * g] * inv_l, oacc[dt][4 * g + 1] * inv_l,
                                       oacc[dt][4 * g + 2] * inv_l, oacc[dt][4 * g + 3] * inv_l);
                 *reinterpret_cast<u32x2*>(orow + d0 * EB) = v;
@@ -977,16 +990,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 static int pick_group(int n_rep) { return (n_rep % 4 == 0) ? 4 : (n_rep % 2 == 0) ? 2 : 1; }
 
-template <typename E, bool PAGED, bool FUSED>
-static hipError_t launch_gf(int G, const PrefillArgs& a, hipStream_t st) {
+template <typename E, bool PAGED, bool FUSED, bool FULLD>
+static hipError_t launch_gfd(int G, const PrefillArgs& a, hipStream_t st) {
     const int grid = (FUSED ? a.decode_blocks : 0) + ((a.total_work + 7) / 8) * 8;
     switch (G) {
-        case 1: hipLaunchKernelGGL((attention_mfma_kernel<E, 1, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL((attention_mfma_kernel<E, 2, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL((attention_mfma_kernel<E, 4, PAGED, FUSED>), dim3(grid), dim3(256), 0, st, a); break;
+        case 1:
+            hipLaunchKernelGGL((attention_mfma_kernel<E, 1, PAGED, FUSED, FULLD>), dim3(grid), dim3(256), 0, st, a);
+            break;
+        case 2:
+            hipLaunchKernelGGL((attention_mfma_kernel<E, 2, PAGED, FUSED, FULLD>), dim3(grid), dim3(256), 0, st, a);
+            break;
+        case 4:
+            hipLaunchKernelGGL((attention_mfma_kernel<E, 4, PAGED, FUSED, FULLD>), dim3(grid), dim3(256), 0, st, a);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <typename E, bool PAGED, bool FUSED>
+static hipError_t launch_gf(int G, const PrefillArgs& a, hipStream_t st) {
+    if (a.head_dim == kDimHead) return launch_gfd<E, PAGED, FUSED, true>(G, a, st);
+    if constexpr (PAGED) {
+        if (a.head_dim >= 16 && a.head_dim < kDimHead && a.head_dim % 16 == 0)
+            return launch_gfd<E, PAGED, FUSED, false>(G, a, st);
+    }
+    return hipErrorInvalidValue;  // dense attention takes exactly 128
 }
 
 template <typename E, bool PAGED>

@@ -21,7 +21,9 @@ Differences from the reference, all supersets: f32 decode is accepted (the
 reference dispatches f16/bf16 only), and the decode kernel splits long
 contexts internally, so ``max_kv_len`` only sizes the split workspace (the
 ``kMaxKVLenNonSplit`` check is kept for API parity; ``femtovllm._DEV.split_kv_decode``
-lifts it).  head_dim must be exactly 128 (the reference accepts <= 128).
+lifts it).  head_dim is at most 128 as the reference checks, in whole 16-byte
+chunks for decode and in multiples of 16 for prefill; dense attention takes
+exactly 128, as the reference's.
 """
 
 from __future__ import annotations
@@ -155,7 +157,7 @@ def _prefill_workspace(device: torch.device, num_seqs: int, num_tokens: int, max
     return _cached_workspace(_prefill_workspaces, device, nbytes, zero=True)
 
 
-def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q, any_head_dim=False):
+def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q, decode=False):
     for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
         _check(t.is_cuda, f"{fn}: {name} must be a GPU tensor")
     if require_contiguous_q:
@@ -174,16 +176,15 @@ def _check_paged(fn, q, k_pool, v_pool, tables, kv_lens, require_contiguous_q, a
     for name, t in (("kv_page_tables", tables), ("kv_lens", kv_lens)):
         _check(t.device == q.device, f"{fn}: {name} must be on {q.device}")
     _check(k_pool.size(2) == kKVLenPerPage, f"{fn}: block_size must be {kKVLenPerPage}, got {k_pool.size(2)}")
-    if any_head_dim:
-        # Decode: head_dim <= 128, TORCH_CHECK_LE(dim_d, kDimHead) (paged_attention_gemv.cu:256-257), in
-        # whole 16-byte chunks (the wave loads rows 16 bytes per lane).
-        _check(q.size(-1) <= kDimHead, f"{fn}: head_dim must be <= {kDimHead}, got {q.size(-1)}")
+    # head_dim <= 128, TORCH_CHECK_LE(dim_d, kDimHead) (paged_attention_gemv.cu:256-257,
+    # paged_attention_gemm.cu:347-348); decode in whole 16-byte chunks (the wave loads rows 16 bytes
+    # per lane), prefill in multiples of 16 (one step of the score MFMAs).
+    _check(q.size(-1) <= kDimHead, f"{fn}: head_dim must be <= {kDimHead}, got {q.size(-1)}")
+    if decode:
         _check((q.size(-1) * q.element_size()) % 16 == 0,
                f"{fn}: head_dim must be a multiple of 16 bytes ({16 // q.element_size()} elements), got {q.size(-1)}")
     else:
-        # Prefill: the MFMA tiling is built for exactly 128, the head_dim of every model the engine runs
-        # (the reference's checks accept <= 128, paged_attention_gemm.cu:348).
-        _check(q.size(-1) == kDimHead, f"{fn}: head_dim must be {kDimHead}, got {q.size(-1)}")
+        _check(q.size(-1) % 16 == 0, f"{fn}: head_dim must be a multiple of 16, got {q.size(-1)}")
     _check(q.size(0) % k_pool.size(1) == 0, f"{fn}: n_heads must be a multiple of n_kv_heads")
 
 
@@ -193,7 +194,7 @@ def _paged_attention_gemv(q, k_pool, v_pool, kv_page_tables, kv_lens, max_kv_len
     ``kMaxKVLenNonSplit`` check (paged_attention_gemv.cu:271-274); ``None``
     lifts it, since the kernel splits contexts of any length over waves."""
     fn = "PagedAttentionGemvCuda"
-    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q, any_head_dim=True)
+    _check_paged(fn, q, k_pool, v_pool, kv_page_tables, kv_lens, require_contiguous_q, decode=True)
     n_heads, num_seqs, dim = q.shape
     _check(num_seqs == kv_page_tables.size(0), f"{fn}: q.size(1) must equal kv_page_tables.size(0)")
     _check(num_seqs == kv_lens.size(0), f"{fn}: q.size(1) must equal kv_lens.size(0)")

@@ -97,6 +97,28 @@ def test_gemm_rejects_fp32(C):
     assert "not implemented for 'Float'" in C._lib.femto_attn_last_error().decode()
 
 
+def _gemm(C, **kw):
+    a = dict(dtype=2, q=16, qsh=128, qst=128, out=16, osh=128, ost=128, k=16, v=16, nb=8, kvh=8, bs=16, d=128,
+             ps0=16384, ps1=2048, ps2=128, cu=16, nseq=2, ntok=10, maxq=5, h=16, tables=16, npages=4, ts=4,
+             kv_lens=16, pos=16, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return C._lib.femto_paged_attention_gemm(*a.values())
+
+
+def test_gemm_head_dim_rule(C):
+    """Prefill takes head_dim <= 128 as the reference checks (paged_attention_gemm.cu:347-348), in
+    multiples of 16; the checks run before anything touches the (fake) pointers."""
+    last = lambda: C._lib.femto_attn_last_error().decode()
+    assert _gemm(C, d=136) == 2 and "head_dim must be at most 128" in last()
+    assert _gemm(C, d=72, ps2=72) == 2 and "multiple of 16" in last()
+    assert _gemm(C, d=0) == 2 and "head_dim" in last()
+    for d in (16, 64, 112):
+        # accepted; the call then fails on its (deliberately too small) workspace before any launch,
+        # with or without a GPU, so the fake pointers are never used
+        rc = _gemm(C, d=d, ps2=d, ps1=16 * d, ps0=8 * 16 * d, ws=256, wsb=64)
+        assert rc != 0 and "head_dim" not in last(), (d, rc, last())
+
+
 def test_gemm_workspace_size_and_checks(C):
     # The size is one slot per resident workgroup of the current device (0
     # without a device, as here); empty calls and bad head counts need none.

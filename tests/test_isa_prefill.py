@@ -66,8 +66,9 @@ def _blocks(body):
 def test_no_wait_between_tile_copies(tmp_path):
     asm = _compile_to_asm(tmp_path)
     kernels = list(_kernels(asm))
-    # {bf16, f16} x G {1, 2, 4} x {paged, paged with decode workers, dense}
-    assert len(kernels) == 18
+    # {bf16, f16} x G {1, 2, 4} x {paged, paged with decode workers, dense} at head_dim 128, and
+    # the paged ones again for head_dim < 128
+    assert len(kernels) == 30
     bad, blocks_with_copies = [], 0
     for name, body in kernels:
         for bname, ins in _blocks(body):

@@ -271,3 +271,35 @@ def test_mixed_batch_tp8_share_both_routes(ops, gpu):
     torch.cuda.synchronize()
     assert_close(torch.cat([outp, outd], dim=1), want, torch.bfloat16, "tp8 share mixed batch, two calls",
                  mask=mask)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [16, 48, 64, 96, 112])
+def test_prefill_head_dim_below_128(ops, gpu, monkeypatch, dtype, head_dim):
+    """head_dim < 128 in multiples of 16, as the reference's check allows (TORCH_CHECK_LE(dim_d, kDimHead),
+    csrc/paged_attention/paged_attention_gemm.cu:347-348): fresh prompts, cached prefixes, a key-split
+    long sequence and one-token rows (the fused decode workers), against the oracle and against the
+    call without key split; the pools' unused blocks and tail rows are NaN."""
+    from test_prefill_split_gpu import _unsplit
+
+    chunks = [(0, 70), (300, 45), (5000, 96), (17, 1), (2000, 1), (0, 1), (64, 33)]
+    H, KVH = 16, 8 if head_dim != 48 else 4
+    w = workloads.make_paged_workload("hd", chunks, H, KVH, head_dim=head_dim, dtype=dtype, seed=head_dim)
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    assert out.shape == (H, q.shape[1], head_dim)
+    want = oracle_prefill(q, meta, w.k_pool, w.v_pool)
+    what = f"prefill head_dim {head_dim} {dtype}"
+    assert_close(out, want, dtype, what)
+    ref = _unsplit(ops, q.to(gpu), meta, wd, monkeypatch)
+    assert_close(out, ref.float().cpu().numpy(), dtype, what + " vs unsplit")
+
+
+@pytest.mark.parametrize("head_dim", [136, 72, 8])
+def test_prefill_head_dim_rejects(ops, gpu, head_dim):
+    w = workloads.make_paged_workload("hdx", [(10, 20)], 8, 8, head_dim=head_dim, seed=3)
+    q, meta = w.gemm_call(device=gpu)
+    wd = w.to(gpu)
+    with pytest.raises(RuntimeError, match="head_dim must be"):
+        run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
