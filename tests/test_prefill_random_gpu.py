@@ -136,3 +136,35 @@ def test_random_batch_arbitrary_positions(ops, gpu, monkeypatch, seed):
     both = ~(np.isnan(a) | np.isnan(b))
     assert np.array_equal(np.isnan(a), np.isnan(b)), what + ": NaN rows differ from the unsplit call"
     assert np.all(np.abs(a - b)[both] <= 1e-2 + ulp * np.maximum(np.abs(a), np.abs(b))[both]), what + " vs unsplit"
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+def test_random_batch_head_dims(ops, gpu, monkeypatch, seed):
+    """The same kind of batches at a head_dim below 128 (a multiple of 16, as the reference's CUDA
+    prefill check allows, csrc/paged_attention/paged_attention_gemm.cu:347-348)."""
+    chunks, H, KVH, dtype = random_batch(7600 + seed)
+    D = int(np.random.default_rng(7600 + seed).choice([16, 32, 48, 64, 80, 96, 112]))
+    what = f"seed {7600 + seed}: H={H} KVH={KVH} D={D} {dtype} chunks {chunks}"
+    print(what, flush=True)
+    w = workloads.make_paged_workload("random_hd", chunks, H, KVH, head_dim=D, dtype=dtype, seed=7600 + seed)
+    q, meta = w.gemm_call(device=gpu)
+    q = q.to(gpu)
+    wd = w.to(gpu)
+    out = _gemm(ops, q, meta, wd)
+    assert out.shape[-1] == D
+    assert _workspace_is_zero(gpu), f"split counters not reset after {what}"
+    cu = meta.raw_cu_seqlens
+    work = sum((cu[b + 1] - cu[b]) * (p + n) for b, (p, n) in enumerate(chunks)) * H
+    rows = None
+    if work > FULL_CHECK:
+        rows = sorted(set(sample_rows(cu, 12, np.random.default_rng(seed))))
+    want = oa.paged_prefill(np64(q.cpu()), np32(w.k_pool), np32(w.v_pool), cu, np_tables(meta),
+                            meta.kv_lens.tolist(), np.asarray(meta.raw_positions), rows=rows)
+    mask = None
+    if rows is not None:
+        mask = np.zeros(want.shape, dtype=bool)
+        mask[:, rows] = True
+    assert_close(out, want, dtype, what, mask=mask)
+    ref = _unsplit(ops, q, meta, wd, monkeypatch)
+    assert_close(out, ref.float().cpu().numpy(), dtype, what + " vs unsplit")
