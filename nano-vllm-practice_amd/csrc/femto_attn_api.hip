@@ -232,12 +232,17 @@ static int paged_decode_entry(const char* fn_name, int dtype, const void* q, int
     femto::DecodePlan plan = femto::plan_paged_decode(n_heads, n_kv_heads, max_kv_len, dtype);
     if (max_kv_len <= g_single_max_kv.load(std::memory_order_relaxed)) {
         // One launch, no workspace.  A max_kv_len below the true longest
-        // context only makes the call slower (each wave walks a quarter of
-        // its sequence, whatever the length).
-        const femto::DecodeArgs a = femto::decode_args(
+        // context only makes the call slower (each wave walks its share of
+        // the sequence, whatever the length).  With at most 256 (sequence,
+        // query head) pairs the workgroups do not fill the GPU: one query
+        // head per wave and eight waves per workgroup halve each wave's pages.
+        const bool wide = (int64_t)num_seqs * n_heads <= 256;
+        if (wide) plan.nrep_tile = 1;
+        femto::DecodeArgs a = femto::decode_args(
             plan, q, q_stride_head, q_stride_seq, out, out_stride_head, out_stride_seq, k_pool, v_pool, num_blocks,
             n_kv_heads, head_dim, pool_stride_block, pool_stride_head, pool_stride_row, kv_page_tables,
             num_pages_per_seq, table_stride, kv_lens, num_seqs, n_heads, nullptr);
+        a.single_waves = wide ? 8 : 4;
         return hip_status(femto::launch_paged_decode(dtype, a, plan.nrep_tile, num_seqs, true,
                                                      static_cast<hipStream_t>(stream)),
                           (fn + " launch").c_str());

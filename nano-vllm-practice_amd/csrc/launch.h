@@ -28,6 +28,7 @@ struct DecodeArgs {
     int min_chunk_pages;  // lower bound on a wave's slice length
     int max_slots;        // partial slots per (sequence, head)
     int head_dim;         // 128, or a smaller multiple of 16 bytes (decode calls only)
+    int single_waves;     // one-launch kernel: waves per workgroup (4, or 8 with one query head per wave)
     float scale_log2;
     float* part_acc;  // [num_seqs][n_heads][max_slots][128]
     float* part_ml;   // [num_seqs][n_heads][max_slots][2]

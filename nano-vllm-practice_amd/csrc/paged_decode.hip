@@ -37,15 +37,18 @@ __global__ __launch_bounds__(256) void paged_decode_kernel(DecodeArgs a) {
     decode_waves<E, NREP, FULL>(a, blockIdx.x);
 }
 
-// One-launch decode for calls of short contexts: one workgroup per (sequence,
-// KV head group), its four waves each taking a contiguous quarter of the
-// sequence's pages; the waves fold their states through LDS and write the
-// normalised rows, so no workspace and no merge launch are needed.  Decode
-// calls only (query row b, kv_lens[b] keys).
-template <typename E, int NREP, bool FULL>
-__global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) {
-    __shared__ float s_ml[4][NREP][2];
-    __shared__ float s_acc[4][NREP][kDimHead];
+// One-launch decode for calls of short contexts: one workgroup of W waves per
+// (sequence, KV head group), wave w taking the w-th of W contiguous shares
+// of the sequence's pages; the waves fold their states through LDS and
+// write the normalised rows, so no workspace and no merge launch are needed.
+// Decode calls only (query row b, kv_lens[b] keys).  W = 4; calls with few
+// (sequence, query head) pairs run one query head per wave with W = 8, so
+// each wave walks half as many pages (a wave's page math, not the loads,
+// sets the length of such a call).
+template <typename E, int NREP, bool FULL, int W>
+__global__ __launch_bounds__(64 * W) void paged_decode_single_kernel(DecodeArgs a) {
+    __shared__ float s_ml[W][NREP][2];
+    __shared__ float s_acc[W][NREP][kDimHead];
     const int b = blockIdx.x, grp = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, rg = lane >> 4;
@@ -53,7 +56,7 @@ __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) 
     const int h0 = kvh * a.n_rep + (grp - kvh * a.head_groups) * NREP;
     const int kv_len = a.kv_lens[b];
     const int npg = pages_of(kv_len);
-    const int per = (npg + 3) >> 2;
+    const int per = (npg + W - 1) / W;
     const int lp0 = min(npg, wave * per), lp1 = min(npg, lp0 + per);
     float m[NREP], l[NREP], acc[NREP][8];
     if (lp1 > lp0) {
@@ -81,7 +84,7 @@ __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) 
     }
     __syncthreads();
     char* out = reinterpret_cast<char*>(a.out);
-    for (int i = threadIdx.x; i < NREP * kDimHead; i += 256) {
+    for (int i = threadIdx.x; i < NREP * kDimHead; i += 64 * W) {
         const int r = i / kDimHead, d = i - r * kDimHead;
         if (!FULL && d >= a.head_dim) continue;
         const int64_t o = (int64_t)(h0 + r) * a.out_stride_head + (int64_t)b * a.out_stride_seq + d;
@@ -91,10 +94,10 @@ __global__ __launch_bounds__(256) void paged_decode_single_kernel(DecodeArgs a) 
         }
         float M = kEmptyMax;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][r][0]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, s_ml[w][r][0]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float f = fast_exp2(s_ml[w][r][0] - M);
             L = fmaf(s_ml[w][r][1], f, L);
             O = fmaf(s_acc[w][r][d], f, O);
@@ -202,8 +205,15 @@ hipError_t launch_paged_decode_merge(int dtype, const DecodeArgs& a, int num_seq
 template <typename E, int NREP, bool FULL>
 static hipError_t launch_t(DecodeArgs a, int num_seqs, bool single, hipStream_t st) {
     if (single) {
-        hipLaunchKernelGGL((paged_decode_single_kernel<E, NREP, FULL>), dim3(num_seqs, a.grid_heads), dim3(256), 0, st,
-                           a);
+        if constexpr (NREP == 1) {
+            if (a.single_waves == 8) {
+                hipLaunchKernelGGL((paged_decode_single_kernel<E, 1, FULL, 8>), dim3(num_seqs, a.grid_heads),
+                                   dim3(512), 0, st, a);
+                return hipGetLastError();
+            }
+        }
+        hipLaunchKernelGGL((paged_decode_single_kernel<E, NREP, FULL, 4>), dim3(num_seqs, a.grid_heads), dim3(256), 0,
+                           st, a);
         return hipGetLastError();
     }
     const int grid = decode_worker_blocks(a);
