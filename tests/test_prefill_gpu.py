@@ -112,6 +112,25 @@ def test_long_context_chunks_every_row(ops, gpu, long_context, chunk):
     print(f"chunk {chunk}: max abs err {err:.2e}")
 
 
+def test_long_context_whole_prompt_one_call(ops, gpu, long_context):
+    """The 32,768-token sequence as one fresh prompt in a single call, the largest chunk a call takes
+    here (1,024 query tiles per KV head, 16 dispatch rounds of the resident slots): sampled rows, the
+    edges of the first and of several later query tiles, and the last rows, which see every key."""
+    w, wd, kp, vp = long_context
+    q, meta = workloads.long_context_chunk(w, 0, chunk=32768, device=gpu)
+    assert q.shape[1] == 32768 and meta.kv_lens.tolist() == [32768]
+    out = run_gemm(ops, q, meta, wd.k_pool, wd.v_pool, gpu)
+    rows = set(sample_rows(meta.raw_cu_seqlens, 40, np.random.default_rng(32768)))
+    rows.update({2047, 2048, 16383, 16384, 32735, 32736, 32766})
+    rows = sorted(rows)
+    want = oa.paged_prefill(np64(q), kp, vp, meta.raw_cu_seqlens, np_tables(meta), meta.kv_lens.tolist(),
+                            np.asarray(meta.raw_positions), rows=rows)
+    mask = np.zeros(want.shape, dtype=bool)
+    mask[:, rows] = True
+    err = assert_close(out, want, torch.bfloat16, "32k-token prompt in one call", mask=mask)
+    print(f"32k prompt, {len(rows)} rows: max abs err {err:.2e}")
+
+
 @pytest.fixture(scope="module")
 def mixed(gpu):
     """The unified Qwen3-8B-shaped batch and the oracle for every row of it.
