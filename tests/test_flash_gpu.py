@@ -74,6 +74,22 @@ def test_dense_attention_random_shapes(C, gpu, seed):
     assert_close(out, want, dtype, f"dense B={B} H={H} KVH={KVH} Tq={Tq} Tkv={Tkv} {dtype}")
 
 
+@pytest.mark.parametrize("tkv", [2048, 8192, 32768])
+def test_dense_attention_long_key_shapes(C, gpu, tkv):
+    """q 1 x 32 x 2048 against k/v 1 x 8 x tkv in bf16 (the long-key shapes the dense entry is timed
+    on), on 40 query rows, tile edges included; rows of a dense call are independent, so the oracle
+    runs on the sampled rows alone."""
+    q = rand((1, 32, 2048, 128), torch.bfloat16, 11)
+    k = rand((1, 8, tkv, 128), torch.bfloat16, 12)
+    v = rand((1, 8, tkv, 128), torch.bfloat16, 13)
+    out = C.FlashAttentionWarpCuda(q.to(gpu), k.to(gpu), v.to(gpu))
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(tkv)
+    rows = sorted({0, 31, 32, 63, 64, 127, 128, 2047} | {int(x) for x in rng.integers(0, 2048, size=32)})
+    want = oa.dense_attention(np64(q[:, :, rows]), np64(k), np64(v))
+    assert_close(out[:, :, rows], want, torch.bfloat16, f"dense q 2048 x 32 heads, Tkv={tkv}")
+
+
 def test_dense_equals_paged_identity_table(C, ops, gpu):
     """Dense attention == paged prefill with contiguous pages and no causal limit."""
     B, H, KVH, T = 1, 8, 4, 96
