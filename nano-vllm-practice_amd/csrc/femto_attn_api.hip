@@ -126,9 +126,27 @@ int scratch_pointer(const std::string& fn, void** ptr) {
     return FEMTO_OK;
 }
 
+std::atomic<int> g_cu_count[kMaxDevices] = {};
+
 }  // namespace
 
 namespace femto {
+
+hipError_t device_cu_count(int& cus) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    int n = g_cu_count[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        if (n <= 0) n = 1;
+        g_cu_count[dev].store(n, std::memory_order_relaxed);  // every thread stores the same value
+    }
+    cus = n;
+    return hipSuccess;
+}
 
 DecodePlan plan_paged_decode(int n_heads, int n_kv_heads, int max_kv_len, int dtype) {
     DecodePlan p;

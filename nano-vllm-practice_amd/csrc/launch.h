@@ -41,6 +41,10 @@ struct DecodeArgs {
     const int32_t* positions;
 };
 
+// Compute units of the current device, queried once per device (safe to call
+// from several host threads).
+hipError_t device_cu_count(int& cus);
+
 // Work split of a decode call.
 struct DecodePlan {
     int nrep_tile;        // query heads per wave

@@ -174,14 +174,8 @@ __global__ __launch_bounds__(128) void paged_decode_merge_kernel(DecodeArgs a) {
 // 3-12 % slower with the dot2 page math).  Sets a.waves_per_group and returns
 // the workgroups of 4 waves that cover the workers (0 on a device error).
 int decode_worker_blocks(DecodeArgs& a) {
-    static int cu_count[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 0;
-    int& cus = cu_count[dev & 63];
-    if (cus == 0) {
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-        if (cus <= 0) cus = 1;
-    }
+    int cus = 0;
+    if (device_cu_count(cus) != hipSuccess) return 0;
     const int total_waves = cus * 4;
     a.waves_per_group = total_waves / a.grid_heads > 0 ? total_waves / a.grid_heads : 1;
     return (a.waves_per_group * a.grid_heads + 3) / 4;

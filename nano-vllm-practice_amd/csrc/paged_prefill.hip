@@ -1041,16 +1041,9 @@ static int prefill_items_per_group(int num_seqs, int num_tokens, int BT) { retur
 
 hipError_t prefill_resident_workgroups(int& resident) {
     // Two workgroups per CU are resident (LDS and register budget).
-    static int cu_count[64] = {0};
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
+    int cus = 0;
+    const hipError_t e = device_cu_count(cus);
     if (e != hipSuccess) return e;
-    int& cus = cu_count[dev & 63];
-    if (cus == 0) {
-        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        if (cus <= 0) cus = 1;
-    }
     resident = 2 * cus;
     return hipSuccess;
 }
