@@ -79,18 +79,19 @@ def row_bound(want: np.ndarray, dtype: torch.dtype) -> np.ndarray:
     return np.broadcast_to(ROW_REL[dtype] * m + half_ulp(m, dtype), want.shape)
 
 
-def assert_close(got: torch.Tensor, want: np.ndarray, dtype: torch.dtype, what: str = "", mask=None):
-    """Max-abs (ATOL / RTOL) and per-row scale-aware (ROW_REL) parity; returns the max abs error."""
+def assert_close(got: torch.Tensor, want: np.ndarray, dtype: torch.dtype, what: str = "", mask=None, factor=1.0):
+    """Max-abs (ATOL / RTOL) and per-row scale-aware (ROW_REL) parity; returns the max abs error.
+    ``factor`` scales both bounds (assert_agree)."""
     g = got if isinstance(got, np.ndarray) else np64(got)
     w = np.asarray(want, dtype=np.float64)
-    rb = row_bound(w, dtype)
+    rb = factor * row_bound(w, dtype)
     if mask is not None:
         g, w, rb = g[mask], w[mask], rb[mask]
     nan_g, nan_w = np.isnan(g), np.isnan(w)
     assert np.array_equal(nan_g, nan_w), f"{what}: NaN pattern differs ({nan_g.sum()} vs {nan_w.sum()})"
     ok = ~nan_w
     err = np.abs(g[ok] - w[ok])
-    tol = ATOL[dtype] + RTOL[dtype] * np.abs(w[ok]) + half_ulp(np.abs(w[ok]), dtype)
+    tol = factor * (ATOL[dtype] + RTOL[dtype] * np.abs(w[ok]) + half_ulp(np.abs(w[ok]), dtype))
     worst = float(err.max()) if err.size else 0.0
     rbo = rb[ok]
     ratio = float((err / np.where(rbo > 0, rbo, np.inf)).max()) if err.size else 0.0
@@ -105,11 +106,22 @@ def assert_close(got: torch.Tensor, want: np.ndarray, dtype: torch.dtype, what: 
     if log:
         with open(log, "a") as f:
             f.write(json.dumps(rec) + "\n")
-    assert np.all(err <= tol), (f"{what}: max abs err {worst:.3e} exceeds tolerance (atol {ATOL[dtype]}, "
-                                f"rtol {RTOL[dtype]}, + half an output ulp)")
-    assert ratio <= 1.0, (f"{what}: error reaches {ratio:.2f}x the per-row bound "
-                          f"({ROW_REL[dtype]:.2e} x max|row| + half ulp); relative RMS error {rel_rms:.2e}")
+    assert np.all(err <= tol), (f"{what}: max abs err {worst:.3e} exceeds tolerance ({factor:g} x (atol "
+                                f"{ATOL[dtype]}, rtol {RTOL[dtype]}, + half an output ulp))")
+    assert ratio <= 1.0, (f"{what}: error reaches {ratio:.2f}x the per-row bound ({factor:g} x "
+                          f"({ROW_REL[dtype]:.2e} x max|row| + half ulp)); relative RMS error {rel_rms:.2e}")
     return worst
+
+
+def assert_agree(got: torch.Tensor, other: torch.Tensor, dtype: torch.dtype, what: str = "", mask=None):
+    """Two kernel results for the same call (e.g. with and without the key split), each of which must
+    lie within the bounds of assert_close from the exact value: by the triangle inequality they differ
+    by at most twice those bounds, which is what this checks.  Each result's own check is against the
+    oracle; this one catches a path that is consistently off where the oracle checks only sample rows.
+    (Seen on random batches: 1 of 1,800 split / unsplit pairs differs by 1.03x a single bound while
+    both pass the oracle.)"""
+    o = other if isinstance(other, np.ndarray) else np64(other)
+    return assert_close(got, o, dtype, what, mask=mask, factor=2.0)
 
 
 def sample_rows(cu_seqlens, per_seq: int, rng: np.random.Generator, tile: int = 32):

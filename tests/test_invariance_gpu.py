@@ -22,7 +22,7 @@ import torch
 
 from femtovllm import workloads
 from femtovllm.metadata import build_varlen_metadata
-from helpers import assert_close
+from helpers import assert_agree, assert_close
 
 pytestmark = pytest.mark.gpu
 
@@ -99,7 +99,7 @@ def test_gqa_equals_replicated_mha(ops, gpu, dtype):
         q, meta = x.gemm_call(device=gpu)
         outs.append(_gemm(ops, q.to(gpu), meta, x.to(gpu)))
     # Same math per row; only how rows are grouped into waves differs.
-    assert_close(outs[0], outs[1].float().cpu().numpy(), dtype, "GQA vs replicated MHA (prefill)")
+    assert_agree(outs[0], outs[1], dtype, "GQA vs replicated MHA (prefill)")
 
     d = workloads.make_paged_workload("gqa_mha_dec", [(900, 1), (33, 1), (4095, 1)], 16, 8, dtype=dtype, seed=46)
     dm = _replicated_kv(d)
@@ -107,7 +107,7 @@ def test_gqa_equals_replicated_mha(ops, gpu, dtype):
     for x in (d, dm):
         q, meta = x.gemv_call(device=gpu)
         outs.append(_gemv(ops, q.to(gpu), meta, x.to(gpu)))
-    assert_close(outs[0], outs[1].float().cpu().numpy(), dtype, "GQA vs replicated MHA (decode)")
+    assert_agree(outs[0], outs[1], dtype, "GQA vs replicated MHA (decode)")
 
 
 @pytest.mark.parametrize("heads", [(16, 8), (32, 8)])

@@ -512,6 +512,28 @@ def test_row_bound_has_power_at_131072_keys():
             assert_close(scaled, want, torch.bfloat16, f"oracle x {factor}")
 
 
+def test_agree_allows_the_sum_of_two_bounds():
+    """Two results 0.9 of a row bound from the exact value on opposite sides each pass
+    assert_close and pass assert_agree (1.8 bounds apart); results 1.1 bounds from it on
+    opposite sides (2.2 apart) fail both."""
+    from helpers import assert_agree, assert_close, row_bound
+
+    rng = np.random.default_rng(5)
+    want = rng.standard_normal((4, 64, 128)) * 0.01
+    rb = row_bound(want, torch.float32)
+    for k, ok in ((0.9, True), (1.1, False)):
+        a, b = want + k * rb, want - k * rb
+        if ok:
+            assert_close(a, want, torch.float32, "a")
+            assert_close(b, want, torch.float32, "b")
+            assert_agree(a, b, torch.float32, "a vs b")
+        else:
+            with pytest.raises(AssertionError):
+                assert_close(a, want, torch.float32, "a")
+            with pytest.raises(AssertionError, match="per-row bound"):
+                assert_agree(a, b, torch.float32, "a vs b")
+
+
 # ---------------------------------------------------------------------------
 # The reference kernel's own precision (oracle/ref_arith.py) and the max-abs
 # bound of the parity helper.

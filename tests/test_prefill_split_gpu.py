@@ -16,7 +16,7 @@ import torch
 
 import oracle.attention as oa
 from femtovllm import workloads
-from helpers import assert_close, np32, np64, np_tables, sample_rows
+from helpers import assert_agree, assert_close, np32, np64, np_tables, sample_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -101,7 +101,7 @@ def _check(ops, w, gpu, monkeypatch, rows_per_seq=6, what=""):
     ref = _unsplit(ops, q, meta, wd, monkeypatch)
     multi = np.ones(want.shape, dtype=bool)
     multi[:, one] = False
-    assert_close(out, ref.float().cpu().numpy(), w.dtype, what + " vs unsplit", mask=multi)
+    assert_agree(out, ref, w.dtype, what + " vs unsplit", mask=multi)
     return err
 
 
@@ -282,9 +282,9 @@ def test_split_values_beyond_fp16_range(ops, gpu, monkeypatch, dtype):
     out = _gemm(ops, q, meta, wd)
     out_big = _gemm(ops, q, meta, big)
     assert torch.isfinite(out_big).all()
-    assert_close(out_big.float() / scale, out.float().cpu().numpy(), dtype, "V x 2^k, split")
+    assert_agree(out_big.float() / scale, out, dtype, "V x 2^k, split")
     ref_big = _unsplit(ops, q, meta, big, monkeypatch)
-    assert_close(out_big.float() / scale, (ref_big.float() / scale).cpu().numpy(), dtype, "V x 2^k vs unsplit")
+    assert_agree(out_big.float() / scale, ref_big.float() / scale, dtype, "V x 2^k vs unsplit")
     assert _workspace_is_zero(gpu)
 
 
