@@ -58,8 +58,10 @@ def test_generator_reaches_every_kind_of_sequence():
     assert split >= 32
 
 
+# range(64), plus seed 3865 (batch 10865: 64 / 8 heads, bf16, eight sequences), whose split and
+# unsplit results differ by slightly more than one row bound while both lie within the oracle's.
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed", range(64))
+@pytest.mark.parametrize("seed", [*range(64), 3865])
 def test_random_batch(ops, gpu, monkeypatch, seed):
     chunks, H, KVH, dtype = random_batch(7000 + seed)
     what = f"seed {7000 + seed}: H={H} KVH={KVH} {dtype} chunks {chunks}"
